@@ -1,0 +1,581 @@
+// extern "C" entry points of libpisa_hip.so (declared in include/pisa_hip.h):
+// argument validation, workspace carving and kernel orchestration.  Nothing
+// here allocates device memory or synchronises: every call enqueues its
+// kernels on the caller's stream and returns.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <mutex>
+#include <string>
+
+
+#include "kernels.hpp"
+
+namespace pisa_host {
+
+static thread_local std::string g_last_error;
+
+void set_error(const char* fmt, ...) {
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+}
+
+int fail(int status, const char* fmt, ...) {
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return status;
+}
+
+int check_launch(const char* what) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(PISA_ERR_LAUNCH, "%s launch failed: %s", what, hipGetErrorString(e));
+    return PISA_OK;
+}
+
+bool valid_dtype(int dtype) { return dtype == PISA_DTYPE_BF16 || dtype == PISA_DTYPE_F16; }
+
+static int elem_size(int dtype) { return dtype == PISA_DTYPE_F32 ? 4 : 2; }
+
+// The library ships gfx950 code objects only; refuse other devices with a
+// clear message instead of a launch failure.
+static int check_device() {
+    static std::mutex mu;
+    static int cached[64];
+    static bool init = false;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return fail(PISA_ERR_DEVICE, "hipGetDevice failed");
+    if (dev < 0 || dev >= 64) return fail(PISA_ERR_DEVICE, "device index %d out of range", dev);
+    std::lock_guard<std::mutex> lock(mu);
+    if (!init) {
+        for (int i = 0; i < 64; ++i) cached[i] = -1;
+        init = true;
+    }
+    if (cached[dev] < 0) {
+        hipDeviceProp_t prop;
+        if (hipGetDeviceProperties(&prop, dev) != hipSuccess)
+            return fail(PISA_ERR_DEVICE, "hipGetDeviceProperties failed for device %d", dev);
+        cached[dev] = strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : 0;
+        if (!cached[dev]) {
+            set_error("device %d is %s; this library is built for gfx950 only", dev, prop.gcnArchName);
+            return PISA_ERR_DEVICE;
+        }
+    }
+    if (!cached[dev]) return fail(PISA_ERR_DEVICE, "device %d is not gfx950; this library is built for gfx950 only", dev);
+    return PISA_OK;
+}
+
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+static int check_view(const char* name, const pisa_view& v, int esize, bool vec16) {
+    if (!v.data) return fail(PISA_ERR_INVALID_ARGUMENT, "%s is null", name);
+    if (vec16) {
+        if (!aligned16(v.data)) return fail(PISA_ERR_INVALID_ARGUMENT, "%s must be 16-byte aligned", name);
+        const int64_t unit = 16 / esize;
+        if (v.batch_stride % unit || v.head_stride % unit || v.token_stride % unit)
+            return fail(PISA_ERR_INVALID_ARGUMENT, "%s strides must be multiples of %lld elements", name, (long long)unit);
+    }
+    return PISA_OK;
+}
+
+static int check_grid(const pisa_token_grid& g, int tokens) {
+    if (g.frames <= 0) return PISA_OK;
+    if (g.height <= 0 || g.width <= 0 || g.height % 8 || g.width % 8)
+        return fail(PISA_ERR_INVALID_ARGUMENT, "token grid height/width must be positive multiples of 8");
+    if ((int64_t)g.frames * g.height * g.width != tokens)
+        return fail(PISA_ERR_INVALID_ARGUMENT, "token grid %dx%dx%d does not match %d tokens", g.frames, g.height,
+                    g.width, tokens);
+    return PISA_OK;
+}
+
+static pisa::View to_view(const pisa_view& v, int heads) {
+    pisa::View r;
+    r.data = static_cast<const char*>(v.data);
+    r.sb = v.batch_stride;
+    r.sh = v.head_stride;
+    r.st = v.token_stride;
+    r.heads = heads;
+    return r;
+}
+
+static pisa::OutView to_out(const pisa_view& v, int heads) {
+    pisa::OutView r;
+    r.data = static_cast<char*>(v.data);
+    r.sb = v.batch_stride;
+    r.sh = v.head_stride;
+    r.st = v.token_stride;
+    r.heads = heads;
+    return r;
+}
+
+// ---- workspace carving
+struct Carver {
+    char* base;
+    int64_t off = 0;
+    explicit Carver(void* b) : base(static_cast<char*>(b)) {}
+    template <typename P> P* take(int64_t bytes) {
+        P* p = base ? reinterpret_cast<P*>(base + off) : nullptr;
+        off += (bytes + 255) & ~int64_t(255);
+        return p;
+    }
+};
+
+struct StatsPlan {
+    int blocks, npad, chunks, chunk_blocks, mask_words;
+};
+
+static StatsPlan plan_stats(int bh, int tokens) {
+    StatsPlan p;
+    p.blocks = (tokens + pisa::kBlock - 1) / pisa::kBlock;
+    p.npad = (p.blocks + 63) / 64 * 64;
+    int target = (512 + bh - 1) / bh;
+    if (target < 1) target = 1;
+    if (target > p.blocks) target = p.blocks;
+    p.chunk_blocks = (p.blocks + target - 1) / target;
+    p.chunks = (p.blocks + p.chunk_blocks - 1) / p.chunk_blocks;
+    p.mask_words = (p.blocks + 31) / 32;
+    return p;
+}
+
+struct ForwardBuffers {
+    void* qc;
+    float* qc_route;
+    float* kc;
+    void* vm;
+    float* hnorm;
+    float* hpart;
+    void* vt;
+    void* kbar_pad;
+    void* vbar_t_pad;
+    void* ht;
+    int32_t* idx;
+    uint32_t* selmask;
+    int64_t total;
+};
+
+static ForwardBuffers carve_forward(void* ws, int bh, int tokens, int head_dim, int exact, int esize) {
+    const StatsPlan p = plan_stats(bh, tokens);
+    const int64_t nd = (int64_t)bh * p.blocks * head_dim;
+    Carver c(ws);
+    ForwardBuffers f;
+    f.qc = c.take<void>(nd * esize);
+    f.qc_route = c.take<float>(nd * 4);
+    f.kc = c.take<float>(nd * 4);
+    f.vm = c.take<void>(nd * esize);
+    f.hnorm = c.take<float>((int64_t)bh * p.blocks * 4);
+    f.hpart = c.take<float>((int64_t)bh * p.chunks * head_dim * head_dim * 4);
+    f.vt = c.take<void>(nd * pisa::kBlock * esize);
+    f.kbar_pad = c.take<void>((int64_t)bh * p.npad * head_dim * esize);
+    f.vbar_t_pad = c.take<void>((int64_t)bh * p.npad * head_dim * esize);
+    f.ht = c.take<void>((int64_t)bh * head_dim * head_dim * esize);
+    f.idx = c.take<int32_t>((int64_t)bh * p.blocks * (exact > 0 ? exact : 1) * 4);
+    f.selmask = c.take<uint32_t>((int64_t)bh * p.blocks * p.mask_words * 4);
+    f.total = c.off;
+    return f;
+}
+
+static bool workspace_ok(void* ws, int64_t have, int64_t need) { return need == 0 || (ws && have >= need && aligned16(ws)); }
+
+}  // namespace pisa_host
+
+using namespace pisa_host;
+
+extern "C" {
+
+int pisa_hip_api_version(void) { return PISA_HIP_API_VERSION; }
+
+const char* pisa_hip_status_string(int status) {
+    switch (status) {
+        case PISA_OK: return "ok";
+        case PISA_ERR_INVALID_ARGUMENT: return "invalid argument";
+        case PISA_ERR_UNSUPPORTED: return "unsupported configuration";
+        case PISA_ERR_WORKSPACE: return "workspace too small";
+        case PISA_ERR_LAUNCH: return "kernel launch failed";
+        case PISA_ERR_DEVICE: return "unsupported device";
+        default: return "unknown status";
+    }
+}
+
+const char* pisa_hip_last_error(void) { return g_last_error.c_str(); }
+
+int pisa_hip_build_info(char* buffer, int64_t capacity) {
+    char info[512];
+    const int n = snprintf(info, sizeof(info),
+                           "api=%d;architecture=gfx950;implementation=hip_mfma_fused_pisa;"
+                           "hip_build_version=%d.%d.%d;block_size=%d;head_dim=128;max_blocks=%d",
+                           PISA_HIP_API_VERSION, HIP_VERSION_MAJOR, HIP_VERSION_MINOR, HIP_VERSION_PATCH,
+                           PISA_BLOCK_SIZE, pisa::kMaxRouteBlocks);
+    if (!buffer || capacity <= n) return fail(PISA_ERR_INVALID_ARGUMENT, "build_info buffer too small");
+    memcpy(buffer, info, n + 1);
+    return PISA_OK;
+}
+
+int64_t pisa_hip_forward_workspace_bytes(int32_t batch, int32_t heads, int32_t tokens, int32_t head_dim,
+                                         int32_t exact_blocks) {
+    if (batch <= 0 || heads <= 0 || tokens <= 0 || head_dim <= 0) return 0;
+    return carve_forward(nullptr, batch * heads, tokens, head_dim, exact_blocks, 2).total;
+}
+
+int pisa_hip_forward(int32_t dtype, int32_t batch, int32_t heads, int32_t tokens, int32_t head_dim, pisa_view q,
+                     pisa_view k, pisa_view v, pisa_view out, pisa_token_grid grid, int32_t exact_blocks, float scale,
+                     int32_t sink_block, int32_t stats_mode, int32_t route_mode, int32_t first_order,
+                     int32_t* debug_indices, float* debug_scores, void* workspace, int64_t workspace_bytes,
+                     void* stream) {
+    if (!valid_dtype(dtype)) return fail(PISA_ERR_UNSUPPORTED, "PISA forward supports bf16 and fp16 only");
+    if (batch <= 0 || heads <= 0 || tokens <= 0)
+        return fail(PISA_ERR_INVALID_ARGUMENT, "PISA forward requires B>0, H>0, T>0");
+    if (head_dim != 128) return fail(PISA_ERR_UNSUPPORTED, "PISA forward requires head_dim=128, got %d", head_dim);
+    const int bh = batch * heads;
+    const StatsPlan p = plan_stats(bh, tokens);
+    if (p.blocks > pisa::kMaxRouteBlocks)
+        return fail(PISA_ERR_UNSUPPORTED, "PISA forward supports at most %d blocks, got %d", pisa::kMaxRouteBlocks, p.blocks);
+    if (exact_blocks < 0 || exact_blocks >= p.blocks)
+        return fail(PISA_ERR_INVALID_ARGUMENT, "exact_blocks must be in [0,%d) for the sparse path, got %d", p.blocks,
+                    exact_blocks);
+    if (sink_block != PISA_NO_SINK && sink_block != 0 && sink_block != -1)
+        return fail(PISA_ERR_INVALID_ARGUMENT, "sink_block must be None, -1, or 0");
+    if (sink_block != PISA_NO_SINK && exact_blocks == 0)
+        return fail(PISA_ERR_INVALID_ARGUMENT, "sink_block requires at least one exact block");
+    if (!(scale > 0.0f) || scale == __builtin_inff()) return fail(PISA_ERR_INVALID_ARGUMENT, "scale must be positive and finite");
+    if (stats_mode != PISA_STATS_HYD && stats_mode != PISA_STATS_GENERIC)
+        return fail(PISA_ERR_INVALID_ARGUMENT, "stats_mode must be HYD or GENERIC");
+    if (route_mode != PISA_ROUTE_HYD && route_mode != PISA_ROUTE_CENTROID)
+        return fail(PISA_ERR_INVALID_ARGUMENT, "route_mode must be HYD or CENTROID");
+    int rc;
+    if ((rc = check_grid(grid, tokens)) || (rc = check_view("q", q, 2, true)) || (rc = check_view("k", k, 2, true)) ||
+        (rc = check_view("v", v, 2, true)) || (rc = check_view("out", out, 2, false)))
+        return rc;
+    if (out.token_stride % 4 || out.head_stride % 4 || out.batch_stride % 4 || (reinterpret_cast<uintptr_t>(out.data) & 7))
+        return fail(PISA_ERR_INVALID_ARGUMENT, "out must be 8-byte aligned with strides multiple of 4 elements");
+    const ForwardBuffers need = carve_forward(nullptr, bh, tokens, head_dim, exact_blocks, 2);
+    if (!workspace_ok(workspace, workspace_bytes, need.total))
+        return fail(PISA_ERR_WORKSPACE, "workspace of %lld bytes (16-byte aligned) required, got %lld",
+                    (long long)need.total, (long long)workspace_bytes);
+    if ((rc = check_device())) return rc;
+
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const ForwardBuffers w = carve_forward(workspace, bh, tokens, head_dim, exact_blocks, 2);
+    const pisa::TokenMap map = pisa::make_token_map(grid);
+
+    pisa::StatsArgs sa;
+    sa.q = to_view(q, heads);
+    sa.k = to_view(k, heads);
+    sa.v = to_view(v, heads);
+    sa.map = map;
+    sa.tokens = tokens;
+    sa.blocks = p.blocks;
+    sa.chunk_blocks = p.chunk_blocks;
+    sa.chunks = p.chunks;
+    sa.qc_out = w.qc;
+    sa.qc_f32 = 0;
+    sa.kc_out = w.kc;
+    sa.vm_out = w.vm;
+    sa.vm_f32 = 0;
+    sa.hnorm_out = w.hnorm;
+    sa.hpart = w.hpart;
+    sa.qc_route = w.qc_route;
+    sa.vt_blocks = w.vt;
+    sa.kbar_pad = w.kbar_pad;
+    sa.vbar_t_pad = w.vbar_t_pad;
+    sa.npad = p.npad;
+    if ((rc = pisa::launch_stats(dtype, stats_mode, sa, bh, st))) return rc;
+
+    pisa::ReduceArgs ra;
+    ra.hpart = w.hpart;
+    ra.chunks = p.chunks;
+    ra.hsum = nullptr;
+    ra.ht = first_order ? w.ht : nullptr;
+    ra.kbar_pad = w.kbar_pad;
+    ra.vbar_t_pad = w.vbar_t_pad;
+    ra.blocks = p.blocks;
+    ra.npad = p.npad;
+    if ((rc = pisa::launch_stats_reduce(dtype, ra, bh, st))) return rc;
+
+    pisa::RouteArgs ro;
+    ro.qc = w.qc_route;
+    ro.kc = w.kc;
+    ro.hnorm = route_mode == PISA_ROUTE_HYD ? w.hnorm : nullptr;
+    ro.rows = bh * p.blocks;
+    ro.blocks = p.blocks;
+    ro.head_dim = head_dim;
+    ro.round_bf16 = route_mode == PISA_ROUTE_HYD ? 1 : 0;
+    ro.sink = sink_block;
+    ro.k = exact_blocks;
+    ro.scale = scale;
+    ro.idx = w.idx;
+    ro.scores = debug_scores;
+    ro.selmask = w.selmask;
+    ro.mask_words = p.mask_words;
+    if ((rc = pisa::launch_route(ro, st))) return rc;
+    if (debug_indices && exact_blocks > 0) {
+        if (hipMemcpyAsync(debug_indices, w.idx, (size_t)bh * p.blocks * exact_blocks * 4, hipMemcpyDeviceToDevice, st) !=
+            hipSuccess)
+            return fail(PISA_ERR_LAUNCH, "copy of debug indices failed");
+    }
+
+    pisa::AttnArgs aa;
+    aa.q = to_view(q, heads);
+    aa.k = to_view(k, heads);
+    aa.o = to_out(out, heads);
+    aa.vt = static_cast<const char*>(w.vt);
+    aa.qmap = map;
+    aa.kmap = map;
+    aa.q_tokens = tokens;
+    aa.kv_tokens = tokens;
+    aa.q_blocks = p.blocks;
+    aa.kv_blocks = p.blocks;
+    aa.scale_log2 = scale * pisa::kLog2e;
+    aa.idx = w.idx;
+    aa.exact = exact_blocks;
+    aa.kbar = static_cast<const char*>(w.kbar_pad);
+    aa.vbar_t = static_cast<const char*>(w.vbar_t_pad);
+    aa.selmask = w.selmask;
+    aa.mask_words = p.mask_words;
+    aa.npad = p.npad;
+    aa.centroids = p.blocks;
+    const int last_len = tokens - (p.blocks - 1) * pisa::kBlock;
+    aa.last_len_log2 = log2f(static_cast<float>(last_len));
+    aa.ht = first_order ? static_cast<const char*>(w.ht) : nullptr;
+    aa.corr_scale = scale / static_cast<float>(tokens);
+    return pisa::launch_attention(dtype, head_dim, true, true, aa, bh, st);
+}
+
+int64_t pisa_hip_block_stats_workspace_bytes(int32_t batch, int32_t heads, int32_t tokens, int32_t head_dim) {
+    if (batch <= 0 || heads <= 0 || tokens <= 0 || head_dim <= 0) return 0;
+    const StatsPlan p = plan_stats(batch * heads, tokens);
+    return (int64_t)batch * heads * p.chunks * head_dim * head_dim * 4;
+}
+
+int pisa_hip_block_stats(int32_t dtype, int32_t out_dtype, int32_t batch, int32_t heads, int32_t tokens,
+                         int32_t head_dim, pisa_view q, pisa_view k, pisa_view v, pisa_token_grid grid,
+                         int32_t stats_mode, void* q_centroids, float* k_centroids, void* v_means, float* h_sum,
+                         float* h_norm, void* workspace, int64_t workspace_bytes, void* stream) {
+    if (!valid_dtype(dtype)) return fail(PISA_ERR_UNSUPPORTED, "block statistics support bf16 and fp16 only");
+    if (out_dtype != dtype && out_dtype != PISA_DTYPE_F32)
+        return fail(PISA_ERR_INVALID_ARGUMENT, "out_dtype must equal dtype or be float32");
+    if (batch <= 0 || heads <= 0 || tokens <= 0) return fail(PISA_ERR_INVALID_ARGUMENT, "requires B>0, H>0, T>0");
+    if (head_dim != 128) return fail(PISA_ERR_UNSUPPORTED, "block statistics require head_dim=128, got %d", head_dim);
+    if (stats_mode != PISA_STATS_MEANS && stats_mode != PISA_STATS_HYD && stats_mode != PISA_STATS_GENERIC)
+        return fail(PISA_ERR_INVALID_ARGUMENT, "unknown stats_mode %d", stats_mode);
+    if (!q_centroids || !k_centroids || !v_means) return fail(PISA_ERR_INVALID_ARGUMENT, "centroid outputs are required");
+    const bool cov = stats_mode != PISA_STATS_MEANS;
+    if (cov && (!h_sum || !h_norm)) return fail(PISA_ERR_INVALID_ARGUMENT, "h_sum and h_norm are required");
+    int rc;
+    if ((rc = check_grid(grid, tokens)) || (rc = check_view("q", q, 2, true)) || (rc = check_view("k", k, 2, true)) ||
+        (rc = check_view("v", v, 2, true)))
+        return rc;
+    const int bh = batch * heads;
+    const StatsPlan p = plan_stats(bh, tokens);
+    const int64_t need = cov ? pisa_hip_block_stats_workspace_bytes(batch, heads, tokens, head_dim) : 0;
+    if (!workspace_ok(workspace, workspace_bytes, need))
+        return fail(PISA_ERR_WORKSPACE, "workspace of %lld bytes required, got %lld", (long long)need,
+                    (long long)workspace_bytes);
+    if ((rc = check_device())) return rc;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    pisa::StatsArgs sa;
+    memset(&sa, 0, sizeof(sa));
+    sa.q = to_view(q, heads);
+    sa.k = to_view(k, heads);
+    sa.v = to_view(v, heads);
+    sa.map = pisa::make_token_map(grid);
+    sa.tokens = tokens;
+    sa.blocks = p.blocks;
+    sa.chunk_blocks = p.chunk_blocks;
+    sa.chunks = p.chunks;
+    sa.qc_out = q_centroids;
+    sa.qc_f32 = out_dtype == PISA_DTYPE_F32;
+    sa.kc_out = k_centroids;
+    sa.vm_out = v_means;
+    sa.vm_f32 = out_dtype == PISA_DTYPE_F32;
+    sa.hnorm_out = cov ? h_norm : nullptr;
+    sa.hpart = cov ? static_cast<float*>(workspace) : nullptr;
+    sa.npad = p.npad;
+    if ((rc = pisa::launch_stats(dtype, stats_mode, sa, bh, st))) return rc;
+    if (!cov) return PISA_OK;
+    pisa::ReduceArgs ra;
+    memset(&ra, 0, sizeof(ra));
+    ra.hpart = static_cast<float*>(workspace);
+    ra.chunks = p.chunks;
+    ra.hsum = h_sum;
+    ra.blocks = p.blocks;
+    ra.npad = p.npad;
+    return pisa::launch_stats_reduce(dtype, ra, bh, st);
+}
+
+int pisa_hip_route_topk(int32_t batch_heads, int32_t blocks, int32_t head_dim, const float* qc, const float* kc,
+                        const float* h_norm, int32_t round_bf16, float scale, int32_t sink_block, int32_t exact_blocks,
+                        int32_t* indices, float* scores, void* stream) {
+    if (batch_heads <= 0 || blocks <= 0) return fail(PISA_ERR_INVALID_ARGUMENT, "requires BH>0 and blocks>0");
+    if (blocks > pisa::kMaxRouteBlocks) return fail(PISA_ERR_UNSUPPORTED, "at most %d blocks", pisa::kMaxRouteBlocks);
+    if (head_dim <= 0 || head_dim > 256 || head_dim % 4)
+        return fail(PISA_ERR_UNSUPPORTED, "head_dim must be a multiple of 4 in (0, 256]");
+    if (exact_blocks < 0 || exact_blocks > blocks) return fail(PISA_ERR_INVALID_ARGUMENT, "exact_blocks out of range");
+    if (sink_block != PISA_NO_SINK && sink_block != 0 && sink_block != -1)
+        return fail(PISA_ERR_INVALID_ARGUMENT, "sink_block must be None, -1, or 0");
+    if (!qc || !kc || (!indices && exact_blocks > 0)) return fail(PISA_ERR_INVALID_ARGUMENT, "null pointer argument");
+    if (!aligned16(kc)) return fail(PISA_ERR_INVALID_ARGUMENT, "kc must be 16-byte aligned");
+    int rc;
+    if ((rc = check_device())) return rc;
+    pisa::RouteArgs ro;
+    ro.qc = qc;
+    ro.kc = kc;
+    ro.hnorm = h_norm;
+    ro.rows = batch_heads * blocks;
+    ro.blocks = blocks;
+    ro.head_dim = head_dim;
+    ro.round_bf16 = round_bf16 ? 1 : 0;
+    ro.sink = sink_block;
+    ro.k = exact_blocks;
+    ro.scale = scale;
+    ro.idx = indices;
+    ro.scores = scores;
+    ro.selmask = nullptr;
+    ro.mask_words = 0;
+    return pisa::launch_route(ro, static_cast<hipStream_t>(stream));
+}
+
+int pisa_hip_pack_spatial_qkv(int32_t dtype, int32_t batch, int32_t heads, int32_t tokens, int32_t head_dim,
+                              pisa_view q, pisa_view k, pisa_view v, pisa_token_grid grid, void* packed_q,
+                              void* packed_k, void* packed_v, void* stream) {
+    if (!valid_dtype(dtype)) return fail(PISA_ERR_UNSUPPORTED, "pack supports bf16 and fp16 only");
+    if (batch <= 0 || heads <= 0 || tokens <= 0) return fail(PISA_ERR_INVALID_ARGUMENT, "requires B>0, H>0, T>0");
+    if (head_dim <= 0 || head_dim % 8 || head_dim > 2048)
+        return fail(PISA_ERR_UNSUPPORTED, "head_dim must be a multiple of 8 (<= 2048)");
+    int rc;
+    if ((rc = check_grid(grid, tokens)) || (rc = check_view("q", q, 2, true)) || (rc = check_view("k", k, 2, true)) ||
+        (rc = check_view("v", v, 2, true)))
+        return rc;
+    if (!packed_q || !packed_k || !packed_v || !aligned16(packed_q) || !aligned16(packed_k) || !aligned16(packed_v))
+        return fail(PISA_ERR_INVALID_ARGUMENT, "packed outputs must be non-null and 16-byte aligned");
+    if ((rc = check_device())) return rc;
+    pisa::LayoutArgs la;
+    la.in[0] = to_view(q, heads);
+    la.in[1] = to_view(k, heads);
+    la.in[2] = to_view(v, heads);
+    la.out[0] = static_cast<char*>(packed_q);
+    la.out[1] = static_cast<char*>(packed_k);
+    la.out[2] = static_cast<char*>(packed_v);
+    la.ntensors = 3;
+    la.map = pisa::make_token_map(grid);
+    la.tokens = tokens;
+    la.head_dim = head_dim;
+    la.heads = heads;
+    return pisa::launch_pack(dtype, la, batch * heads, static_cast<hipStream_t>(stream));
+}
+
+int pisa_hip_unpack_spatial_output(int32_t dtype, int32_t batch, int32_t heads, int32_t tokens, int32_t head_dim,
+                                   const void* packed, pisa_token_grid grid, void* raster, void* stream) {
+    if (!valid_dtype(dtype)) return fail(PISA_ERR_UNSUPPORTED, "unpack supports bf16 and fp16 only");
+    if (batch <= 0 || heads <= 0 || tokens <= 0) return fail(PISA_ERR_INVALID_ARGUMENT, "requires B>0, H>0, T>0");
+    if (head_dim <= 0 || head_dim % 8 || head_dim > 2048)
+        return fail(PISA_ERR_UNSUPPORTED, "head_dim must be a multiple of 8 (<= 2048)");
+    int rc;
+    if ((rc = check_grid(grid, tokens))) return rc;
+    if (!packed || !raster || !aligned16(packed) || !aligned16(raster))
+        return fail(PISA_ERR_INVALID_ARGUMENT, "packed and raster must be non-null and 16-byte aligned");
+    if ((rc = check_device())) return rc;
+    return pisa::launch_unpack(dtype, static_cast<const char*>(packed), static_cast<char*>(raster),
+                               pisa::make_token_map(grid), tokens, head_dim, heads, batch * heads,
+                               static_cast<hipStream_t>(stream));
+}
+
+int pisa_hip_fuse_spatial_epilogue(int32_t dtype, int32_t batch, int32_t heads, int32_t tokens, int32_t head_dim,
+                                   const void* exact_output, const float* exact_lse, const void* approximate_output,
+                                   const float* approximate_lse, const float* correction, pisa_token_grid grid,
+                                   void* out, void* stream) {
+    if (!valid_dtype(dtype)) return fail(PISA_ERR_UNSUPPORTED, "epilogue supports bf16 and fp16 only");
+    if (batch <= 0 || heads <= 0 || tokens <= 0) return fail(PISA_ERR_INVALID_ARGUMENT, "requires B>0, H>0, T>0");
+    if (head_dim <= 0 || head_dim % 8 || head_dim > 2048)
+        return fail(PISA_ERR_UNSUPPORTED, "head_dim must be a multiple of 8 (<= 2048)");
+    int rc;
+    if ((rc = check_grid(grid, tokens))) return rc;
+    if (!exact_output || !exact_lse || !approximate_output || !approximate_lse || !correction || !out)
+        return fail(PISA_ERR_INVALID_ARGUMENT, "null pointer argument");
+    if (!aligned16(exact_output) || !aligned16(approximate_output) || !aligned16(correction) || !aligned16(out))
+        return fail(PISA_ERR_INVALID_ARGUMENT, "outputs and correction must be 16-byte aligned");
+    if ((rc = check_device())) return rc;
+    return pisa::launch_merge(dtype, static_cast<const char*>(exact_output), exact_lse,
+                              static_cast<const char*>(approximate_output), approximate_lse, correction,
+                              static_cast<char*>(out), pisa::make_token_map(grid), tokens, head_dim, heads,
+                              batch * heads, static_cast<hipStream_t>(stream));
+}
+
+int64_t attn_hip_dense_workspace_bytes(int32_t batch, int32_t heads, int32_t kv_tokens, int32_t head_dim) {
+    if (batch <= 0 || heads <= 0 || kv_tokens <= 0 || head_dim <= 0) return 0;
+    const int64_t blocks = (kv_tokens + pisa::kBlock - 1) / pisa::kBlock;
+    return (int64_t)batch * heads * blocks * head_dim * pisa::kBlock * 2;
+}
+
+int attn_hip_dense_forward(int32_t dtype, int32_t batch, int32_t heads, int32_t q_tokens, int32_t kv_tokens,
+                           int32_t head_dim, pisa_view q, pisa_view k, pisa_view v, pisa_view out, float scale,
+                           void* workspace, int64_t workspace_bytes, void* stream) {
+    if (!valid_dtype(dtype)) return fail(PISA_ERR_UNSUPPORTED, "dense attention supports bf16 and fp16 only");
+    if (batch <= 0 || heads <= 0 || q_tokens <= 0 || kv_tokens <= 0)
+        return fail(PISA_ERR_INVALID_ARGUMENT, "requires B>0, H>0, Tq>0, Tk>0");
+    if (head_dim != 64 && head_dim != 128)
+        return fail(PISA_ERR_UNSUPPORTED, "dense attention supports head_dim 64 or 128, got %d", head_dim);
+    if (!(scale > 0.0f) || scale == __builtin_inff()) return fail(PISA_ERR_INVALID_ARGUMENT, "scale must be positive and finite");
+    int rc;
+    if ((rc = check_view("q", q, 2, true)) || (rc = check_view("k", k, 2, true)) || (rc = check_view("v", v, 2, true)) ||
+        (rc = check_view("out", out, 2, false)))
+        return rc;
+    if (out.token_stride % 4 || out.head_stride % 4 || out.batch_stride % 4 || (reinterpret_cast<uintptr_t>(out.data) & 7))
+        return fail(PISA_ERR_INVALID_ARGUMENT, "out must be 8-byte aligned with strides multiple of 4 elements");
+    const int64_t need = attn_hip_dense_workspace_bytes(batch, heads, kv_tokens, head_dim);
+    if (!workspace_ok(workspace, workspace_bytes, need))
+        return fail(PISA_ERR_WORKSPACE, "workspace of %lld bytes required, got %lld", (long long)need,
+                    (long long)workspace_bytes);
+    if ((rc = check_device())) return rc;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const int bh = batch * heads;
+    const int kv_blocks = (kv_tokens + pisa::kBlock - 1) / pisa::kBlock;
+    if ((rc = pisa::launch_vt_pack(dtype, head_dim, to_view(v, heads), kv_tokens, kv_blocks, bh,
+                                   static_cast<char*>(workspace), st)))
+        return rc;
+    pisa::AttnArgs aa;
+    memset(&aa, 0, sizeof(aa));
+    aa.q = to_view(q, heads);
+    aa.k = to_view(k, heads);
+    aa.o = to_out(out, heads);
+    aa.vt = static_cast<const char*>(workspace);
+    aa.qmap = pisa::TokenMap{0, 0, 0};
+    aa.kmap = pisa::TokenMap{0, 0, 0};
+    aa.q_tokens = q_tokens;
+    aa.kv_tokens = kv_tokens;
+    aa.q_blocks = (q_tokens + pisa::kBlock - 1) / pisa::kBlock;
+    aa.kv_blocks = kv_blocks;
+    aa.scale_log2 = scale * pisa::kLog2e;
+    return pisa::launch_attention(dtype, head_dim, false, false, aa, bh, st);
+}
+
+int attn_hip_fixed_block_forward(int32_t dtype, int32_t batch, int32_t heads, int32_t tokens, int32_t head_dim,
+                                 int32_t block_size, pisa_view q, pisa_view k, pisa_view v, pisa_view out, float scale,
+                                 int32_t causal, void* stream) {
+    if (dtype != PISA_DTYPE_BF16 && dtype != PISA_DTYPE_F16 && dtype != PISA_DTYPE_F32)
+        return fail(PISA_ERR_UNSUPPORTED, "fixed-block attention supports bf16, fp16 and fp32");
+    if (batch <= 0 || heads <= 0 || tokens <= 0) return fail(PISA_ERR_INVALID_ARGUMENT, "requires B>0, H>0, T>0");
+    if (block_size != 64) return fail(PISA_ERR_UNSUPPORTED, "fixed-block attention supports block_size=64 only");
+    if (head_dim != 32 && head_dim != 64 && head_dim != 128)
+        return fail(PISA_ERR_UNSUPPORTED, "fixed-block attention supports head_dim 32/64/128, got %d", head_dim);
+    if (!(scale == scale) || scale == __builtin_inff() || scale == -__builtin_inff())
+        return fail(PISA_ERR_INVALID_ARGUMENT, "scale must be finite");
+    const int es = elem_size(dtype);
+    int rc;
+    if ((rc = check_view("q", q, es, false)) || (rc = check_view("k", k, es, false)) ||
+        (rc = check_view("v", v, es, false)) || (rc = check_view("out", out, es, false)))
+        return rc;
+    if ((rc = check_device())) return rc;
+    return pisa::launch_fixed_block(dtype, head_dim, to_view(q, heads), to_view(k, heads), to_view(v, heads),
+                                    to_out(out, heads), tokens, batch * heads, scale, causal ? 1 : 0,
+                                    static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

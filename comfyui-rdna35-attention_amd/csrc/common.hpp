@@ -1,0 +1,161 @@
+// Shared device/host helpers for the gfx950 attention kernels.
+//
+// Conventions used by every kernel in this library:
+//   * a wavefront is 64 lanes; `lane = threadIdx.x & 63`, `half = lane >> 5`,
+//     `col = lane & 31` are the coordinates of the 32x32 MFMA layouts;
+//   * v_mfma_f32_32x32x16_{bf16,f16}: lane (half, col) supplies 8 operand
+//     values A[col][slot] / B[slot][col] for the 16-deep contraction slots
+//     half*8 .. half*8+7, and receives accumulator values
+//       D[row = 8*(v/4) + 4*half + (v%4)][col],  v = 0..15;
+//   * key blocks are stored transposed ("V^T blocks", [D][64]) with the key
+//     index bit-permuted by swap23(), so that a lane's 8 accumulator rows of
+//     one MFMA output feed one 16-byte operand load of the next MFMA.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "pisa_hip.h"
+
+namespace pisa {
+
+typedef __bf16 bf16_t;
+typedef _Float16 f16_t;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kBlock = PISA_BLOCK_SIZE;  // tokens per PISA block
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+// ---------------------------------------------------------------- element types
+template <typename T> struct Elem;
+template <> struct Elem<bf16_t> {
+    typedef bf16x8 vec8;
+    static constexpr int dtype = PISA_DTYPE_BF16;
+};
+template <> struct Elem<f16_t> {
+    typedef f16x8 vec8;
+    static constexpr int dtype = PISA_DTYPE_F16;
+};
+
+__device__ __forceinline__ float to_f32(bf16_t x) { return static_cast<float>(x); }
+__device__ __forceinline__ float to_f32(f16_t x) { return static_cast<float>(x); }
+__device__ __forceinline__ float to_f32(float x) { return x; }
+
+template <typename T> __device__ __forceinline__ T from_f32(float x);
+template <> __device__ __forceinline__ bf16_t from_f32<bf16_t>(float x) { return static_cast<bf16_t>(x); }
+template <> __device__ __forceinline__ f16_t from_f32<f16_t>(float x) { return static_cast<f16_t>(x); }
+template <> __device__ __forceinline__ float from_f32<float>(float x) { return x; }
+
+// 32x32x16 MFMA on 8-element operands, fp32 accumulation.
+__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16 mfma32(f16x8 a, f16x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// 16-byte global load / store of 8 elements.
+template <typename V> __device__ __forceinline__ V load8(const void* p) {
+    u32x4 raw = *reinterpret_cast<const u32x4*>(p);
+    return __builtin_bit_cast(V, raw);
+}
+template <typename V> __device__ __forceinline__ void store8(void* p, V v) {
+    *reinterpret_cast<u32x4*>(p) = __builtin_bit_cast(u32x4, v);
+}
+
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
+    return x;
+}
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
+    return x;
+}
+
+// Bits 2 and 3 of a key index swapped: the storage position of key `k`
+// inside a transposed key block (self inverse).
+__host__ __device__ __forceinline__ int swap23(int k) {
+    return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1);
+}
+
+// ---------------------------------------------------------------- views
+struct View {
+    const char* data;  // byte pointer
+    int64_t sb, sh, st;  // element strides
+    int heads;
+    __device__ __forceinline__ int64_t row(int bh, int64_t token) const {
+        const int b = bh / heads;
+        const int h = bh - b * heads;
+        return b * sb + h * sh + token * st;
+    }
+};
+
+struct OutView {
+    char* data;
+    int64_t sb, sh, st;
+    int heads;
+    __device__ __forceinline__ int64_t row(int bh, int64_t token) const {
+        const int b = bh / heads;
+        const int h = bh - b * heads;
+        return b * sb + h * sh + token * st;
+    }
+};
+
+// Block-major position -> raster token (see pisa_token_grid in pisa_hip.h).
+struct TokenMap {
+    int frame_tokens;   // 0: identity
+    int width;
+    int tiles_per_row;
+    __device__ __forceinline__ int operator()(int o) const {
+        if (frame_tokens == 0) return o;
+        const int f = o / frame_tokens;
+        const int w = o - f * frame_tokens;
+        const int tile = w >> 6;
+        const int intra = w & 63;
+        const int tr = tile / tiles_per_row;
+        const int tc = tile - tr * tiles_per_row;
+        return f * frame_tokens + ((tr << 3) + (intra >> 3)) * width + (tc << 3) + (intra & 7);
+    }
+};
+
+inline TokenMap make_token_map(const pisa_token_grid& g) {
+    TokenMap m;
+    if (g.frames <= 0) {
+        m.frame_tokens = 0;
+        m.width = 0;
+        m.tiles_per_row = 0;
+    } else {
+        m.frame_tokens = g.height * g.width;
+        m.width = g.width;
+        m.tiles_per_row = g.width / 8;
+    }
+    return m;
+}
+
+// Wavefront -> logical work index so that consecutive logical indices land on
+// the same XCD (workgroups are dispatched round robin over the 8 XCDs).
+__device__ __forceinline__ int xcd_remap(int wg, int total) {
+    const int xcd = wg & 7;
+    const int local = wg >> 3;
+    const int base = total >> 3;
+    const int rem = total & 7;
+    return xcd * base + (xcd < rem ? xcd : rem) + local;
+}
+
+}  // namespace pisa
+
+// ---------------------------------------------------------------- host side
+namespace pisa_host {
+void set_error(const char* fmt, ...);
+int fail(int status, const char* fmt, ...);
+int check_launch(const char* what);
+bool valid_dtype(int dtype);
+}  // namespace pisa_host

@@ -1,0 +1,101 @@
+// Argument blocks and launchers of the gfx950 kernels (one translation unit
+// per subsystem; api.hip validates arguments and calls the launchers).
+#pragma once
+
+#include "common.hpp"
+
+namespace pisa {
+
+constexpr int kMaxRouteBlocks = 1024;  // routing row length held in LDS
+
+struct StatsArgs {
+    View q, k, v;
+    TokenMap map;
+    int tokens, blocks, chunk_blocks, chunks;
+    // API outputs
+    void* qc_out;   // [BH][N][D] (f32 when qc_f32)
+    int qc_f32;
+    float* kc_out;  // [BH][N][D]
+    void* vm_out;   // [BH][N][D] (f32 when vm_f32)
+    int vm_f32;
+    float* hnorm_out;  // [BH][N] (nullable)
+    float* hpart;      // [BH][chunks][D][D] (HYD / GENERIC)
+    // attention operands (nullable)
+    float* qc_route;   // [BH][N][D] f32 means for routing
+    void* vt_blocks;   // [BH][N][D][64] transposed V blocks, swap23 key order
+    void* kbar_pad;    // [BH][npad][D] dtype k_bar
+    void* vbar_t_pad;  // [BH][D][npad] dtype v_bar, swap23 centroid order
+    int npad;
+};
+
+// Sums the per-chunk partials in chunk order; writes H_sum (fp32), the
+// transposed dtype copy used by the first-order correction, and zeroes the
+// padding of the centroid tables.
+struct ReduceArgs {
+    const float* hpart;
+    int chunks;
+    float* hsum;       // [BH][D][D] (nullable)
+    void* ht;          // [BH][D][D] dtype, ht[c][r] = dtype(H_sum[r][c]) (nullable)
+    void* kbar_pad;    // nullable
+    void* vbar_t_pad;  // nullable
+    int blocks, npad;
+};
+
+struct RouteArgs {
+    const float* qc;     // [BH][N][D]
+    const float* kc;     // [BH][N][D]
+    const float* hnorm;  // [BH][N] or null
+    int rows, blocks, head_dim, round_bf16, sink, k;
+    float scale;
+    int32_t* idx;        // [BH][N][k]
+    float* scores;       // [BH][N][N] or null
+    uint32_t* selmask;   // [BH][N][mask_words] or null
+    int mask_words;
+};
+
+struct AttnArgs {
+    View q, k;
+    OutView o;
+    const char* vt;   // [BH][kv_blocks][D][64] dtype, swap23 key order
+    TokenMap qmap, kmap;
+    int q_tokens, kv_tokens, q_blocks, kv_blocks;
+    float scale_log2;  // softmax scale * log2(e)
+    // sparse exact chunks
+    const int32_t* idx;  // [BH][q_blocks][exact]
+    int exact;
+    // tail chunks
+    const char* kbar;        // [BH][npad][D] dtype
+    const char* vbar_t;      // [BH][D][npad] dtype, swap23 centroid order
+    const uint32_t* selmask; // [BH][q_blocks][mask_words]
+    int mask_words, npad, centroids;
+    float last_len_log2;     // log2(length of the last block)
+    // first-order correction
+    const char* ht;          // [BH][D][D] dtype, ht[c][r] = H_sum[r][c]
+    float corr_scale;        // s / T
+};
+
+struct LayoutArgs {
+    View in[3];
+    char* out[3];
+    int ntensors;
+    TokenMap map;
+    int tokens, head_dim, heads;
+};
+
+int launch_stats(int dtype, int mode, const StatsArgs& a, int bh_count, hipStream_t stream);
+int launch_stats_reduce(int dtype, const ReduceArgs& a, int bh_count, hipStream_t stream);
+int launch_route(const RouteArgs& a, hipStream_t stream);
+int launch_attention(int dtype, int head_dim, bool sparse, bool tail, const AttnArgs& a, int bh_count,
+                     hipStream_t stream);
+int launch_vt_pack(int dtype, int head_dim, const View& v, int kv_tokens, int kv_blocks, int bh_count, char* vt,
+                   hipStream_t stream);
+int launch_fixed_block(int dtype, int head_dim, const View& q, const View& k, const View& v, const OutView& o,
+                       int tokens, int bh_count, float scale, int causal, hipStream_t stream);
+int launch_pack(int dtype, const LayoutArgs& a, int bh_count, hipStream_t stream);
+int launch_unpack(int dtype, const char* packed, char* out, TokenMap map, int tokens, int head_dim, int heads,
+                  int bh_count, hipStream_t stream);
+int launch_merge(int dtype, const char* exact, const float* exact_lse, const char* approx, const float* approx_lse,
+                 const float* corr, char* out, TokenMap map, int tokens, int head_dim, int heads, int bh_count,
+                 hipStream_t stream);
+
+}  // namespace pisa

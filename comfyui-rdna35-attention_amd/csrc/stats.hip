@@ -1,0 +1,315 @@
+// Subsystem 1: per-64-token-block statistics on gfx950.
+//
+// One 256-thread workgroup owns `chunk_blocks` consecutive key blocks of one
+// (batch, head).  For every block it
+//   * reads the 64 query/key/value rows once (16-byte loads, token order from
+//     the grid map, so raster spatial/video layouts need no packing pass),
+//   * reduces the column sums (lane shuffles + one LDS exchange) into the
+//     block means q_bar, k_bar, v_bar,
+//   * centres the keys in fp32, splits them into a bf16 pair hi + lo and
+//     stages hi, lo and V transposed in LDS,
+//   * computes H_b = (K - k_bar)^T V with 32x32x16 MFMAs (hi and lo passes,
+//     fp32 accumulation), its Frobenius norm, and accumulates H_b into a
+//     per-workgroup partial of H_sum held in the MFMA accumulators,
+//   * writes the transposed V block (the operand layout of the attention
+//     kernel) and the padded centroid tables used by the tail.
+// The partial H_sum of each workgroup is written once; stats_reduce_kernel
+// sums the partials in a fixed order, so H_sum is deterministic (the
+// reference accumulates it with float atomicAdd, pisa_kernels.cu:227).
+//
+// Semantics follow block_stats_hyd_kernel (pisa_kernels.cu:167-244: means are
+// sum-then-scale, keys centred in fp32), block_stats_kernel
+// (pisa_kernels.cu:130-164: every element pre-scaled by 1/len) and the Triton
+// statistics (pisa_kernel.py:49-84: centred keys rounded to the input dtype).
+#include "kernels.hpp"
+
+namespace pisa {
+
+constexpr int kStatsThreads = 256;
+constexpr int kLdsRow = kBlock + 8;  // padded LDS row (elements) of a transposed block
+
+
+template <typename T, int MODE>
+__global__ __launch_bounds__(kStatsThreads) void stats_kernel(StatsArgs a) {
+    constexpr int D = 128;
+    typedef typename Elem<T>::vec8 vec8;
+    __shared__ __attribute__((aligned(16))) T lds_hi[D * kLdsRow];
+    __shared__ __attribute__((aligned(16))) T lds_lo[D * kLdsRow];
+    __shared__ __attribute__((aligned(16))) T lds_v[D * kLdsRow];
+    __shared__ float red[3][4][D];
+    __shared__ float kmean[D];
+    __shared__ float norm_part[4];
+
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = t >> 6;
+    const int half = lane >> 5;
+    const int col = lane & 31;
+    const int c16 = t & 15;        // dims c16*8 .. c16*8+7
+    const int rq = t >> 4;         // tokens rq*4 .. rq*4+3 of the block
+    const int bh = blockIdx.x / a.chunks;
+    const int chunk = blockIdx.x - bh * a.chunks;
+    const int first = chunk * a.chunk_blocks;
+    const int last = min(a.blocks, first + a.chunk_blocks);
+    constexpr bool kCov = MODE != PISA_STATS_MEANS;
+
+    f32x16 hp[4];
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) hp[nt][v] = 0.0f;
+
+    for (int b = first; b < last; ++b) {
+        const int start = b * kBlock;
+        const int len = min(kBlock, a.tokens - start);
+        const float inv_len = 1.0f / static_cast<float>(len);
+
+        // ---- load 4 rows x 8 dims of q, k, v
+        vec8 qv[4], kv[4], vv[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int tok = rq * 4 + r;
+            if (tok < len) {
+                const int raster = a.map(start + tok);
+                const int64_t off = (c16 * 8) * (int64_t)sizeof(T);
+                qv[r] = load8<vec8>(a.q.data + a.q.row(bh, raster) * sizeof(T) + off);
+                kv[r] = load8<vec8>(a.k.data + a.k.row(bh, raster) * sizeof(T) + off);
+                vv[r] = load8<vec8>(a.v.data + a.v.row(bh, raster) * sizeof(T) + off);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    qv[r][e] = T(0.0f);
+                    kv[r][e] = T(0.0f);
+                    vv[r][e] = T(0.0f);
+                }
+            }
+        }
+
+        // ---- column sums over this thread's 4 rows, then over the block
+        float sq[8], sk[8], sv[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            float xq = 0.0f, xk = 0.0f, xv = 0.0f;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                if (MODE == PISA_STATS_MEANS) {
+                    xq += to_f32(qv[r][e]) * inv_len;
+                    xk += to_f32(kv[r][e]) * inv_len;
+                    xv += to_f32(vv[r][e]) * inv_len;
+                } else {
+                    xq += to_f32(qv[r][e]);
+                    xk += to_f32(kv[r][e]);
+                    xv += to_f32(vv[r][e]);
+                }
+            }
+            xq += __shfl_xor(xq, 16);
+            xk += __shfl_xor(xk, 16);
+            xv += __shfl_xor(xv, 16);
+            xq += __shfl_xor(xq, 32);
+            xk += __shfl_xor(xk, 32);
+            xv += __shfl_xor(xv, 32);
+            sq[e] = xq;
+            sk[e] = xk;
+            sv[e] = xv;
+        }
+        if (lane < 16) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                red[0][wave][c16 * 8 + e] = sq[e];
+                red[1][wave][c16 * 8 + e] = sk[e];
+                red[2][wave][c16 * 8 + e] = sv[e];
+            }
+        }
+        __syncthreads();
+        if (t < D) {
+            const int d = t;
+            float mq = ((red[0][0][d] + red[0][1][d]) + red[0][2][d]) + red[0][3][d];
+            float mk = ((red[1][0][d] + red[1][1][d]) + red[1][2][d]) + red[1][3][d];
+            float mv = ((red[2][0][d] + red[2][1][d]) + red[2][2][d]) + red[2][3][d];
+            if (MODE == PISA_STATS_HYD) {
+                mq *= inv_len;
+                mk *= inv_len;
+                mv *= inv_len;
+            } else if (MODE == PISA_STATS_GENERIC) {
+                const float fl = static_cast<float>(len);
+                mq /= fl;
+                mk /= fl;
+                mv /= fl;
+            }
+            kmean[d] = mk;
+            const int64_t o = ((int64_t)bh * a.blocks + b) * D + d;
+            if (a.qc_f32) static_cast<float*>(a.qc_out)[o] = mq;
+            else static_cast<T*>(a.qc_out)[o] = from_f32<T>(mq);
+            a.kc_out[o] = mk;
+            if (a.vm_f32) static_cast<float*>(a.vm_out)[o] = mv;
+            else static_cast<T*>(a.vm_out)[o] = from_f32<T>(mv);
+            if (a.qc_route) a.qc_route[o] = mq;
+            if (a.kbar_pad)
+                static_cast<T*>(a.kbar_pad)[((int64_t)bh * a.npad + b) * D + d] = from_f32<T>(mk);
+            if (a.vbar_t_pad)
+                static_cast<T*>(a.vbar_t_pad)[((int64_t)bh * D + d) * a.npad + swap23(b)] = from_f32<T>(mv);
+        }
+        if (!kCov) {
+            __syncthreads();
+            continue;
+        }
+        __syncthreads();
+
+        // ---- centre keys, stage hi / lo / V transposed (swap23 token order)
+        const int p0 = swap23(rq * 4);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int d = c16 * 8 + e;
+            const float km = kmean[d];
+            T hi[4], lo[4], vt[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const bool valid = rq * 4 + r < len;
+                const float c = valid ? to_f32(kv[r][e]) - km : 0.0f;
+                hi[r] = from_f32<T>(c);
+                lo[r] = (MODE == PISA_STATS_HYD) ? from_f32<T>(c - to_f32(hi[r])) : T(0.0f);
+                vt[r] = vv[r][e];
+            }
+            typedef T vec4 __attribute__((ext_vector_type(4)));
+            vec4 h4 = {hi[0], hi[1], hi[2], hi[3]};
+            vec4 l4 = {lo[0], lo[1], lo[2], lo[3]};
+            vec4 v4 = {vt[0], vt[1], vt[2], vt[3]};
+            *reinterpret_cast<vec4*>(&lds_hi[d * kLdsRow + p0]) = h4;
+            if (MODE == PISA_STATS_HYD) *reinterpret_cast<vec4*>(&lds_lo[d * kLdsRow + p0]) = l4;
+            *reinterpret_cast<vec4*>(&lds_v[d * kLdsRow + p0]) = v4;
+        }
+        __syncthreads();
+
+        // ---- H_b tile rows [32*wave, 32*wave+32) x all 128 columns
+        f32x16 hb[4];
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) hb[nt][v] = 0.0f;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            const int pos = ks * 16 + half * 8;
+            const vec8 ah = *reinterpret_cast<const vec8*>(&lds_hi[(wave * 32 + col) * kLdsRow + pos]);
+            vec8 al;
+            if (MODE == PISA_STATS_HYD)
+                al = *reinterpret_cast<const vec8*>(&lds_lo[(wave * 32 + col) * kLdsRow + pos]);
+#pragma unroll
+            for (int nt = 0; nt < 4; ++nt) {
+                const vec8 bv = *reinterpret_cast<const vec8*>(&lds_v[(nt * 32 + col) * kLdsRow + pos]);
+                hb[nt] = mfma32(ah, bv, hb[nt]);
+                if (MODE == PISA_STATS_HYD) hb[nt] = mfma32(al, bv, hb[nt]);
+            }
+        }
+        float ss = 0.0f;
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                ss += hb[nt][v] * hb[nt][v];
+                hp[nt][v] += hb[nt][v];
+            }
+        ss = wave_sum(ss);
+        if (lane == 0) norm_part[wave] = ss;
+
+        // ---- transposed V block for the attention kernel
+        if (a.vt_blocks) {
+            T* dst = static_cast<T*>(a.vt_blocks) + ((int64_t)bh * a.blocks + b) * D * kBlock;
+#pragma unroll
+            for (int it = 0; it < 4; ++it) {
+                const int id = it * kStatsThreads + t;
+                const int d = id >> 3;
+                const int pc = id & 7;
+                const vec8 x = *reinterpret_cast<const vec8*>(&lds_v[d * kLdsRow + pc * 8]);
+                store8(dst + d * kBlock + pc * 8, x);
+            }
+        }
+        __syncthreads();
+        if (t == 0 && a.hnorm_out)
+            a.hnorm_out[(int64_t)bh * a.blocks + b] =
+                sqrtf(((norm_part[0] + norm_part[1]) + norm_part[2]) + norm_part[3]);
+    }
+
+    if (kCov) {
+        float* dst = a.hpart + ((int64_t)bh * a.chunks + chunk) * D * D;
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int r = wave * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
+                dst[r * D + nt * 32 + col] = hp[nt][v];
+            }
+    }
+}
+
+
+template <typename T>
+__global__ __launch_bounds__(256) void stats_reduce_kernel(ReduceArgs a) {
+    constexpr int D = 128;
+    __shared__ float tile[32][33];
+    const int bh = blockIdx.y;
+    const int tr = blockIdx.x >> 2;  // 32-row tile index
+    const int tc = blockIdx.x & 3;   // 32-col tile index
+    const int t = threadIdx.x;
+    const float* src = a.hpart + (int64_t)bh * a.chunks * D * D;
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+        const int lr = it * 8 + (t >> 5);
+        const int lc = t & 31;
+        const int r = tr * 32 + lr;
+        const int c = tc * 32 + lc;
+        float s = 0.0f;
+        for (int ch = 0; ch < a.chunks; ++ch) s += src[(int64_t)ch * D * D + r * D + c];
+        if (a.hsum) a.hsum[(int64_t)bh * D * D + r * D + c] = s;
+        tile[lr][lc] = s;
+    }
+    __syncthreads();
+    if (a.ht) {
+        T* ht = static_cast<T*>(a.ht) + (int64_t)bh * D * D;
+#pragma unroll
+        for (int it = 0; it < 4; ++it) {
+            const int lr = it * 8 + (t >> 5);  // output row = H column
+            const int lc = t & 31;
+            ht[(tc * 32 + lr) * D + tr * 32 + lc] = from_f32<T>(tile[lc][lr]);
+        }
+    }
+    if (blockIdx.x == 0) {
+        const int pad = a.npad - a.blocks;
+        if (a.kbar_pad)
+            for (int i = t; i < pad * D; i += 256)
+                static_cast<T*>(a.kbar_pad)[((int64_t)bh * a.npad + a.blocks) * D + i] = T(0.0f);
+        if (a.vbar_t_pad)
+            for (int i = t; i < pad * D; i += 256) {
+                const int d = i / pad;
+                const int j = a.blocks + (i - d * pad);
+                static_cast<T*>(a.vbar_t_pad)[((int64_t)bh * D + d) * a.npad + swap23(j)] = T(0.0f);
+            }
+    }
+}
+
+template <typename T, int MODE>
+int launch_stats_t(const StatsArgs& a, int bh_count, hipStream_t stream) {
+    hipLaunchKernelGGL((stats_kernel<T, MODE>), dim3(bh_count * a.chunks), dim3(kStatsThreads), 0,
+                       stream, a);
+    return pisa_host::check_launch("stats_kernel");
+}
+
+int launch_stats(int dtype, int mode, const StatsArgs& a, int bh_count, hipStream_t stream) {
+    if (dtype == PISA_DTYPE_BF16) {
+        if (mode == PISA_STATS_MEANS) return launch_stats_t<bf16_t, PISA_STATS_MEANS>(a, bh_count, stream);
+        if (mode == PISA_STATS_HYD) return launch_stats_t<bf16_t, PISA_STATS_HYD>(a, bh_count, stream);
+        return launch_stats_t<bf16_t, PISA_STATS_GENERIC>(a, bh_count, stream);
+    }
+    if (mode == PISA_STATS_MEANS) return launch_stats_t<f16_t, PISA_STATS_MEANS>(a, bh_count, stream);
+    if (mode == PISA_STATS_HYD) return launch_stats_t<f16_t, PISA_STATS_HYD>(a, bh_count, stream);
+    return launch_stats_t<f16_t, PISA_STATS_GENERIC>(a, bh_count, stream);
+}
+
+int launch_stats_reduce(int dtype, const ReduceArgs& a, int bh_count, hipStream_t stream) {
+    if (dtype == PISA_DTYPE_BF16)
+        hipLaunchKernelGGL(stats_reduce_kernel<bf16_t>, dim3(16, bh_count), dim3(256), 0, stream, a);
+    else
+        hipLaunchKernelGGL(stats_reduce_kernel<f16_t>, dim3(16, bh_count), dim3(256), 0, stream, a);
+    return pisa_host::check_launch("stats_reduce_kernel");
+}
+
+}  // namespace pisa

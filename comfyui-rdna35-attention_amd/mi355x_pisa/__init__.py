@@ -1,0 +1,584 @@
+"""MI355X (gfx950) native PISA attention ops.
+
+Drop-in counterpart of the reference's ``rdna35_pisa_ck`` package
+(native/rdna35_pisa_ck/rdna35_pisa_ck/__init__.py): same entry points
+(``forward``, ``forward_spatial_bhtd``, ``block_stats_hyd``, ``prepare``,
+``build_info``, ``capabilities``, ``clear_compile_cache``), same argument
+meaning, validation messages and error types, registered as
+``torch.library`` custom ops with fake implementations so they trace under
+``torch.compile(fullgraph=True)``.  The work itself runs in hand-written HIP
+kernels (libpisa_hip.so, C ABI in include/pisa_hip.h):
+
+    stats (1 launch) -> H_sum reduction (1) -> routing + top-k (1)
+    -> fused exact + tail + first-order + merge + raster store (1)
+
+instead of the reference's pack / CK stats / bmm / topk / FlexAttention x2 /
+bmm / epilogue sequence.  No Triton, FlexAttention or CK is involved, and
+there is no fallback implementation: if the library is missing, importing
+this package raises.
+"""
+from __future__ import annotations
+
+import math
+import struct
+
+import torch
+
+from . import _lib
+from ._lib import LIB, check, dtype_code, grid, ptr, stream_of, view3, view4
+
+__version__ = "1.0.0"
+
+BLOCK_SIZE = 64
+HEAD_DIM = 128
+MAX_BLOCKS = 1024
+MAX_TOKENS = BLOCK_SIZE * MAX_BLOCKS
+SPATIAL_SIDE = 96
+SPATIAL_TOKENS = SPATIAL_SIDE * SPATIAL_SIDE
+SPATIAL_SPARSE_EXACT_BLOCKS = 23
+ARCHITECTURE = "gfx950"
+_SUPPORTED_DTYPES = {torch.bfloat16}
+
+
+def _float32(value: float) -> float:
+    """Round to float32; positive finite only (__init__.py:80-87)."""
+    try:
+        converted = struct.unpack("f", struct.pack("f", float(value)))[0]
+    except (OverflowError, struct.error, TypeError, ValueError) as exc:
+        raise ValueError("scale must be representable as a positive finite float32 value.") from exc
+    if not math.isfinite(converted) or converted <= 0.0:
+        raise ValueError("scale must be representable as a positive finite float32 value.")
+    return converted
+
+
+def _is_rocm_device(tensor: torch.Tensor) -> bool:
+    return tensor.device.type == "cuda" and torch.version.hip is not None
+
+
+def _validate_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
+    """__init__.py:90-104, with this library's token limit."""
+    if not all(isinstance(tensor, torch.Tensor) for tensor in (q, k, v)):
+        raise TypeError("q, k, and v must be torch tensors.")
+    if q.ndim != 3 or q.shape != k.shape or q.shape != v.shape:
+        raise ValueError("PISA HIP expects matching [BH,T,D] q/k/v tensors.")
+    if q.shape[0] <= 0 or q.shape[1] <= 0 or q.shape[1] > MAX_TOKENS or q.shape[2] != HEAD_DIM:
+        raise ValueError(f"PISA HIP requires BH>0, 0<T<={MAX_TOKENS}, and D={HEAD_DIM}.")
+    if q.device != k.device or q.device != v.device or not _is_rocm_device(q):
+        raise ValueError("PISA HIP requires q/k/v on one PyTorch ROCm device.")
+    if q.dtype not in _SUPPORTED_DTYPES or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError("PISA HIP requires matching bfloat16 q/k/v.")
+    if not q.is_contiguous() or not k.is_contiguous() or not v.is_contiguous():
+        raise ValueError("PISA HIP requires contiguous q/k/v.")
+    if q.requires_grad or k.requires_grad or v.requires_grad:
+        raise ValueError("PISA HIP is forward-only.")
+
+
+def _validate_spatial_bhtd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
+    """__init__.py:107-123."""
+    if not all(isinstance(tensor, torch.Tensor) for tensor in (q, k, v)):
+        raise TypeError("q, k, and v must be torch tensors.")
+    if q.ndim != 4 or q.shape != k.shape or q.shape != v.shape:
+        raise ValueError("PISA spatial HIP expects matching [B,H,T,D] q/k/v tensors.")
+    batch, heads, tokens, head_dim = q.shape
+    if batch <= 0 or heads <= 0 or tokens != SPATIAL_TOKENS or head_dim != HEAD_DIM:
+        raise ValueError(f"PISA spatial HIP requires B>0, H>0, T={SPATIAL_TOKENS}, and D={HEAD_DIM}.")
+    if q.device != k.device or q.device != v.device or not _is_rocm_device(q):
+        raise ValueError("PISA spatial HIP requires q/k/v on one PyTorch ROCm device.")
+    if q.dtype not in _SUPPORTED_DTYPES or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError("PISA spatial HIP requires matching bfloat16 q/k/v.")
+    expected_stride = (tokens * heads * head_dim, head_dim, heads * head_dim, 1)
+    if q.stride() != expected_stride or k.stride() != expected_stride or v.stride() != expected_stride:
+        raise ValueError("PISA spatial HIP requires BHTD views of contiguous [B,T,H,D] storage.")
+    if any(tensor.requires_grad for tensor in (q, k, v)):
+        raise ValueError("PISA spatial HIP is forward-only.")
+
+
+def _check_exact_and_sink(exact_blocks, blocks: int, sink_block) -> None:
+    if isinstance(exact_blocks, bool) or not isinstance(exact_blocks, int):
+        raise TypeError("exact_blocks must be an integer.")
+    if exact_blocks < 0 or exact_blocks > blocks:
+        raise ValueError(f"exact_blocks must be in [0,{blocks}].")
+    if sink_block not in (None, -1, 0):
+        raise ValueError("sink_block must be None, -1, or 0.")
+    if sink_block is not None and exact_blocks == 0:
+        raise ValueError("sink_block requires at least one exact block.")
+
+
+# --------------------------------------------------------------------------- launchers
+def _launch_pisa(q4, k4, v4, out4, token_grid, exact_blocks, scale, sink_block, stats_mode, route_mode,
+                 first_order, debug_indices=None, debug_scores=None):
+    batch, heads, tokens, head_dim = q4.shape
+    with torch.cuda.device(q4.device):
+        ws_bytes = LIB.pisa_hip_forward_workspace_bytes(batch, heads, tokens, head_dim, exact_blocks)
+        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=q4.device)
+        check(
+            LIB.pisa_hip_forward(
+                dtype_code(q4.dtype), batch, heads, tokens, head_dim,
+                view4(q4), view4(k4), view4(v4), view4(out4), token_grid,
+                exact_blocks, scale, sink_block, stats_mode, route_mode, int(first_order),
+                ptr(debug_indices), ptr(debug_scores), workspace.data_ptr(), ws_bytes, stream_of(q4.device),
+            ),
+            "pisa_hip_forward",
+        )
+
+
+def _launch_dense(q4, k4, v4, out4, scale):
+    batch, heads, q_tokens, head_dim = q4.shape
+    kv_tokens = k4.shape[2]
+    with torch.cuda.device(q4.device):
+        ws_bytes = LIB.attn_hip_dense_workspace_bytes(batch, heads, kv_tokens, head_dim)
+        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=q4.device)
+        check(
+            LIB.attn_hip_dense_forward(
+                dtype_code(q4.dtype), batch, heads, q_tokens, kv_tokens, head_dim,
+                view4(q4), view4(k4), view4(v4), view4(out4), scale,
+                workspace.data_ptr(), ws_bytes, stream_of(q4.device),
+            ),
+            "attn_hip_dense_forward",
+        )
+
+
+def _launch_fixed_block(q4, k4, v4, out4, scale, causal):
+    batch, heads, tokens, head_dim = q4.shape
+    with torch.cuda.device(q4.device):
+        check(
+            LIB.attn_hip_fixed_block_forward(
+                dtype_code(q4.dtype), batch, heads, tokens, head_dim, BLOCK_SIZE,
+                view4(q4), view4(k4), view4(v4), view4(out4), scale, int(bool(causal)), stream_of(q4.device),
+            ),
+            "attn_hip_fixed_block_forward",
+        )
+
+
+def _as4(tensor: torch.Tensor) -> torch.Tensor:
+    """[BH,T,D] -> [BH,1,T,D] view."""
+    return tensor.unsqueeze(1)
+
+
+def _forward_impl(q, k, v, exact_blocks, scale, sink_block, token_grid=None, out4=None):
+    """Sparse or dense PISA over [B,H,T,D] views q/k/v (__init__.py:233-316).
+
+    exact_blocks == N is exact dense attention (the reference calls SDPA,
+    __init__.py:251-252); otherwise HYD statistics, HYD routing, exact tiles,
+    centroid tail and first-order correction, merged in one kernel.
+    """
+    batch, heads, tokens, _ = q.shape
+    blocks = (tokens + BLOCK_SIZE - 1) // BLOCK_SIZE
+    if exact_blocks < 0 or exact_blocks > blocks:
+        raise ValueError(f"exact_blocks must be in [0,{blocks}].")
+    if sink_block not in (-2, -1, 0):
+        raise ValueError("sink_block must be None, -1, or 0.")
+    if sink_block != -2 and exact_blocks == 0:
+        raise ValueError("sink_block requires at least one exact block.")
+    if out4 is None:
+        out4 = torch.empty_like(q, memory_format=torch.contiguous_format)
+    if exact_blocks == blocks:
+        _launch_dense(q, k, v, out4, scale)
+    else:
+        _launch_pisa(q, k, v, out4, token_grid or grid(), exact_blocks, scale, sink_block,
+                     _lib.STATS_HYD, _lib.ROUTE_HYD, True)
+    return out4
+
+
+# --------------------------------------------------------------------------- custom ops
+@torch.library.custom_op("mi355x_pisa::forward", mutates_args=(), device_types="cuda")
+def _forward_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, exact_blocks: int, scale: float,
+                sink_block: int) -> torch.Tensor:
+    out = torch.empty_like(q)
+    _forward_impl(_as4(q), _as4(k), _as4(v), exact_blocks, scale, sink_block, out4=_as4(out))
+    return out
+
+
+@_forward_op.register_fake
+def _forward_op_fake(q, k, v, exact_blocks, scale, sink_block):
+    del k, v, exact_blocks, scale, sink_block
+    return torch.empty_like(q)
+
+
+@torch.library.custom_op("mi355x_pisa::forward_spatial_bhtd", mutates_args=(), device_types="cuda")
+def _forward_spatial_bhtd_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, exact_blocks: int, scale: float,
+                             sink_block: int) -> torch.Tensor:
+    batch, heads, tokens, head_dim = q.shape
+    out = q.new_empty((batch, tokens, heads * head_dim))
+    out4 = out.view(batch, tokens, heads, head_dim).permute(0, 2, 1, 3)
+    # Dense attention is order independent, so the exact profile needs no tiling.
+    token_grid = grid(1, SPATIAL_SIDE, SPATIAL_SIDE)
+    _forward_impl(q, k, v, exact_blocks, scale, sink_block, token_grid=token_grid, out4=out4)
+    return out
+
+
+@_forward_spatial_bhtd_op.register_fake
+def _forward_spatial_bhtd_op_fake(q, k, v, exact_blocks, scale, sink_block):
+    del k, v, exact_blocks, scale, sink_block
+    return q.new_empty((q.shape[0], q.shape[2], q.shape[1] * q.shape[3]))
+
+
+@torch.library.custom_op("mi355x_pisa::block_stats_hyd", mutates_args=(), device_types="cuda")
+def _block_stats_hyd_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> tuple[
+        torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    return _block_stats(q, k, v, _lib.STATS_HYD, q.dtype)
+
+
+@_block_stats_hyd_op.register_fake
+def _block_stats_hyd_op_fake(q, k, v):
+    del k, v
+    blocks = (q.shape[1] + BLOCK_SIZE - 1) // BLOCK_SIZE
+    shape = (q.shape[0], blocks, q.shape[2])
+    return (
+        q.new_empty(shape),
+        q.new_empty(shape, dtype=torch.float32),
+        q.new_empty(shape),
+        q.new_empty((q.shape[0], q.shape[2], q.shape[2]), dtype=torch.float32),
+        q.new_empty((q.shape[0], blocks), dtype=torch.float32),
+    )
+
+
+@torch.library.custom_op("mi355x_pisa::generic_forward", mutates_args=(), device_types="cuda")
+def _generic_forward_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, exact_blocks: int, scale: float,
+                        first_order: bool, frames: int, height: int, width: int) -> torch.Tensor:
+    batch, heads, tokens, head_dim = q.shape
+    out = q.new_empty((batch, tokens, heads, head_dim))
+    out4 = out.permute(0, 2, 1, 3)
+    blocks = (tokens + BLOCK_SIZE - 1) // BLOCK_SIZE
+    if exact_blocks == blocks:
+        _launch_dense(q, k, v, out4, scale)
+    else:
+        _launch_pisa(q, k, v, out4, grid(frames, height, width), exact_blocks, scale, -2,
+                     _lib.STATS_GENERIC, _lib.ROUTE_CENTROID, first_order)
+    return out
+
+
+@_generic_forward_op.register_fake
+def _generic_forward_op_fake(q, k, v, exact_blocks, scale, first_order, frames, height, width):
+    del k, v, exact_blocks, scale, first_order, frames, height, width
+    return q.new_empty((q.shape[0], q.shape[2], q.shape[1], q.shape[3]))
+
+
+@torch.library.custom_op("mi355x_pisa::dense_attention", mutates_args=(), device_types="cuda")
+def _dense_attention_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float,
+                        merged_output: bool) -> torch.Tensor:
+    batch, heads, q_tokens, head_dim = q.shape
+    if merged_output:
+        out = q.new_empty((batch, q_tokens, heads * head_dim))
+        out4 = out.view(batch, q_tokens, heads, head_dim).permute(0, 2, 1, 3)
+    else:
+        out = q.new_empty((batch, heads, q_tokens, head_dim))
+        out4 = out
+    _launch_dense(q, k, v, out4, scale)
+    return out
+
+
+@_dense_attention_op.register_fake
+def _dense_attention_op_fake(q, k, v, scale, merged_output):
+    del k, v, scale
+    batch, heads, q_tokens, head_dim = q.shape
+    if merged_output:
+        return q.new_empty((batch, q_tokens, heads * head_dim))
+    return q.new_empty((batch, heads, q_tokens, head_dim))
+
+
+@torch.library.custom_op("mi355x_pisa::fixed_block_attention", mutates_args=(), device_types="cuda")
+def _fixed_block_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float, causal: bool) -> torch.Tensor:
+    out = q.new_empty(q.shape)
+    _launch_fixed_block(q, k, v, out, scale, causal)
+    return out
+
+
+@_fixed_block_op.register_fake
+def _fixed_block_op_fake(q, k, v, scale, causal):
+    del k, v, scale, causal
+    return q.new_empty(q.shape)
+
+
+# --------------------------------------------------------------------------- statistics
+def _block_stats(q, k, v, mode, out_dtype):
+    """q/k/v: [BH,T,D] (or [B,H,T,D] views).  Returns the 5 HYD outputs (3 for MEANS)."""
+    q4 = q if q.ndim == 4 else _as4(q)
+    k4 = k if k.ndim == 4 else _as4(k)
+    v4 = v if v.ndim == 4 else _as4(v)
+    batch, heads, tokens, head_dim = q4.shape
+    bh = batch * heads
+    blocks = (tokens + BLOCK_SIZE - 1) // BLOCK_SIZE
+    shape = (bh, blocks, head_dim)
+    q_centroids = q.new_empty(shape, dtype=out_dtype)
+    k_centroids = q.new_empty(shape, dtype=torch.float32)
+    v_means = q.new_empty(shape, dtype=out_dtype)
+    cov = mode != _lib.STATS_MEANS
+    h_sum = q.new_empty((bh, head_dim, head_dim), dtype=torch.float32) if cov else None
+    h_norm = q.new_empty((bh, blocks), dtype=torch.float32) if cov else None
+    with torch.cuda.device(q.device):
+        ws_bytes = LIB.pisa_hip_block_stats_workspace_bytes(batch, heads, tokens, head_dim) if cov else 0
+        workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
+        check(
+            LIB.pisa_hip_block_stats(
+                dtype_code(q.dtype), dtype_code(out_dtype), batch, heads, tokens, head_dim,
+                view4(q4), view4(k4), view4(v4), grid(), mode,
+                q_centroids.data_ptr(), k_centroids.data_ptr(), v_means.data_ptr(), ptr(h_sum), ptr(h_norm),
+                workspace.data_ptr(), ws_bytes, stream_of(q.device),
+            ),
+            "pisa_hip_block_stats",
+        )
+    if not cov:
+        return q_centroids, k_centroids, v_means
+    return q_centroids, k_centroids, v_means, h_sum, h_norm
+
+
+def block_stats_hyd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor):
+    """(q_bar, k_bar fp32, v_bar, H_sum fp32) of [BH,T,D] q/k/v (__init__.py:216-230)."""
+    if q.ndim != 3 or q.shape != k.shape or q.shape != v.shape:
+        raise ValueError("PISA HIP HYD expects matching [BH,T,D] q/k/v tensors.")
+    if q.shape[0] <= 0 or q.shape[1] <= 0 or q.shape[1] > MAX_TOKENS or q.shape[2] != HEAD_DIM:
+        raise ValueError(f"PISA HIP HYD requires BH>0, 0<T<={MAX_TOKENS}, and D={HEAD_DIM}.")
+    if q.device != k.device or q.device != v.device or not _is_rocm_device(q):
+        raise ValueError("PISA HIP HYD requires q/k/v on one PyTorch ROCm device.")
+    if q.dtype not in (torch.float16, torch.bfloat16) or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError("PISA HIP HYD requires matching fp16/bf16 q/k/v.")
+    if not q.is_contiguous() or not k.is_contiguous() or not v.is_contiguous():
+        raise ValueError("PISA HIP HYD requires contiguous q/k/v.")
+    if q.requires_grad or k.requires_grad or v.requires_grad:
+        raise ValueError("PISA HIP HYD is forward-only.")
+    return _block_stats_hyd_op(q, k, v)[:4]
+
+
+# --------------------------------------------------------------------------- public API
+def forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, exact_blocks: int, scale: float | None = None,
+            sink_block: int | None = None) -> torch.Tensor:
+    """PISA HYD attention of contiguous [BH,T,128] bf16 q/k/v (__init__.py:381-403)."""
+    _validate_qkv(q, k, v)
+    blocks = (q.shape[1] + BLOCK_SIZE - 1) // BLOCK_SIZE
+    _check_exact_and_sink(exact_blocks, blocks, sink_block)
+    scale_value = _float32(1.0 / math.sqrt(HEAD_DIM) if scale is None else scale)
+    return _forward_op(q, k, v, exact_blocks, scale_value, -2 if sink_block is None else sink_block)
+
+
+def forward_spatial_bhtd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, exact_blocks: int,
+                         scale: float | None = None, sink_block: int | None = None) -> torch.Tensor:
+    """Anima spatial PISA: [B,H,9216,128] BHTD views of [B,9216,H,128] storage -> [B,9216,H*128].
+
+    Blocks are the 8x8 tiles of the 96x96 token grid (__init__.py:406-433); the
+    kernels read the raster layout through the tile map and write the raster
+    output directly, so no pack or unpack pass runs.
+    """
+    _validate_spatial_bhtd(q, k, v)
+    blocks = SPATIAL_TOKENS // BLOCK_SIZE
+    if isinstance(exact_blocks, bool) or not isinstance(exact_blocks, int):
+        raise TypeError("exact_blocks must be an integer.")
+    if exact_blocks < 0 or exact_blocks > blocks:
+        raise ValueError(f"exact_blocks must be in [0,{blocks}].")
+    if exact_blocks not in (SPATIAL_SPARSE_EXACT_BLOCKS, blocks):
+        raise ValueError(
+            f"spatial PISA supports exact_blocks={SPATIAL_SPARSE_EXACT_BLOCKS}; "
+            f"use exact_blocks={blocks} only for dense SDPA validation."
+        )
+    _check_exact_and_sink(exact_blocks, blocks, sink_block)
+    scale_value = _float32(1.0 / math.sqrt(HEAD_DIM) if scale is None else scale)
+    return _forward_spatial_bhtd_op(q, k, v, exact_blocks, scale_value, -2 if sink_block is None else sink_block)
+
+
+def generic_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, exact_blocks: int, scale: float,
+                    first_order: bool, token_grid: tuple[int, int, int] | None = None) -> torch.Tensor:
+    """Generic PISA over [B,H,T,D] views (generic_pisa.py:141-232 semantics).
+
+    Centroid routing without the HYD bias, dtype-rounded centred keys for
+    H_sum, optional first-order correction.  token_grid=(frames, height, width)
+    selects per-frame 8x8 tile blocks; the output is [B,T,H,D] contiguous.
+    """
+    frames, height, width = token_grid if token_grid is not None else (0, 0, 0)
+    return _generic_forward_op(q, k, v, int(exact_blocks), float(scale), bool(first_order),
+                               int(frames), int(height), int(width))
+
+
+def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float,
+                    merged_output: bool = False) -> torch.Tensor:
+    """Exact attention of [B,H,Tq,D] q over [B,H,Tk,D] k/v (any strides, unit D stride).
+
+    Returns [B,H,Tq,D] contiguous, or [B,Tq,H*D] when merged_output is set.
+    """
+    return _dense_attention_op(q, k, v, float(scale), bool(merged_output))
+
+
+def fixed_block_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float,
+                          causal: bool = False) -> torch.Tensor:
+    """64-token block-diagonal attention of [B,H,T,D] q/k/v -> [B,H,T,D] contiguous."""
+    return _fixed_block_op(q, k, v, float(scale), bool(causal))
+
+
+def route_topk(q_centroids: torch.Tensor, k_centroids: torch.Tensor, h_norm: torch.Tensor | None,
+               exact_blocks: int, scale: float, sink_block: int | None = None,
+               round_bf16: bool = True) -> tuple[torch.Tensor, torch.Tensor]:
+    """Routing scores [BH,N,N] and ascending top-k indices [BH,N,k] (int32).
+
+    q/k centroids are fp32 [BH,N,D]; h_norm (fp32 [BH,N]) adds ln(h_norm+1e-5).
+    """
+    bh, blocks, head_dim = q_centroids.shape
+    qc = q_centroids.float().contiguous()
+    kc = k_centroids.float().contiguous()
+    hn = None if h_norm is None else h_norm.float().contiguous()
+    indices = torch.empty((bh, blocks, max(exact_blocks, 1)), dtype=torch.int32, device=qc.device)
+    scores = torch.empty((bh, blocks, blocks), dtype=torch.float32, device=qc.device)
+    with torch.cuda.device(qc.device):
+        check(
+            LIB.pisa_hip_route_topk(bh, blocks, head_dim, qc.data_ptr(), kc.data_ptr(), ptr(hn), int(round_bf16),
+                                    float(scale), -2 if sink_block is None else int(sink_block), int(exact_blocks),
+                                    indices.data_ptr(), scores.data_ptr(), stream_of(qc.device)),
+            "pisa_hip_route_topk",
+        )
+    return scores, indices[..., :exact_blocks]
+
+
+def forward_with_routing(q4: torch.Tensor, k4: torch.Tensor, v4: torch.Tensor, exact_blocks: int, scale: float,
+                         sink_block: int | None = None, hyd: bool = True, first_order: bool = True,
+                         token_grid: tuple[int, int, int] | None = None):
+    """Sparse PISA forward that also returns the routing scores and selection.
+
+    Diagnostic entry point for parity checks: (out [B,H,T,D] contiguous,
+    scores fp32 [BH,N,N], indices int32 [BH,N,k]).
+    """
+    batch, heads, tokens, head_dim = q4.shape
+    blocks = (tokens + BLOCK_SIZE - 1) // BLOCK_SIZE
+    out = q4.new_empty(q4.shape)
+    scores = torch.empty((batch * heads, blocks, blocks), dtype=torch.float32, device=q4.device)
+    indices = torch.empty((batch * heads, blocks, max(exact_blocks, 1)), dtype=torch.int32, device=q4.device)
+    frames, height, width = token_grid if token_grid is not None else (0, 0, 0)
+    _launch_pisa(q4, k4, v4, out, grid(frames, height, width), exact_blocks, _float32(scale),
+                 -2 if sink_block is None else sink_block,
+                 _lib.STATS_HYD if hyd else _lib.STATS_GENERIC, _lib.ROUTE_HYD if hyd else _lib.ROUTE_CENTROID,
+                 first_order, debug_indices=indices, debug_scores=scores)
+    return out, scores, indices[..., :exact_blocks]
+
+
+def prepare(device_index: int | None = None) -> None:
+    """Nothing is compiled at run time; only checks that a ROCm device is present."""
+    if not torch.cuda.is_available() or torch.version.hip is None:
+        raise RuntimeError("mi355x-pisa requires a PyTorch ROCm device.")
+    index = torch.cuda.current_device() if device_index is None else int(device_index)
+    torch.cuda.get_device_properties(index)
+
+
+def build_info() -> dict[str, object]:
+    info: dict[str, object] = {}
+    for item in _lib.build_info_string().split(";"):
+        key, _, value = item.partition("=")
+        info[key] = int(value) if value.isdigit() else value
+    info["package_version"] = __version__
+    info["torch_runtime_version"] = torch.__version__
+    info["hip_runtime_version"] = torch.version.hip
+    return info
+
+
+def capabilities() -> dict[str, object]:
+    return {
+        "architecture": ARCHITECTURE,
+        "block_size": BLOCK_SIZE,
+        "head_dim": HEAD_DIM,
+        "max_blocks": MAX_BLOCKS,
+        "dtypes": (torch.bfloat16,),
+        "causal": False,
+        "backward": False,
+        "first_order_tail": True,
+        "first_order_routing_bias": True,
+        "flex_attention": False,
+        "outer_torch_compile": True,
+        "outer_torch_compile_requires_prepare": False,
+        "spatial_bhtd": True,
+        "spatial_tokens": SPATIAL_TOKENS,
+        "spatial_sparse_exact_blocks": (SPATIAL_SPARSE_EXACT_BLOCKS,),
+        "hyd_stats_head_dims": (HEAD_DIM,),
+        "hyd_stats_dtypes": (torch.bfloat16, torch.float16),
+        "generic_head_dims": (HEAD_DIM,),
+        "generic_dtypes": (torch.bfloat16, torch.float16),
+        "dense_head_dims": (64, 128),
+        "fixed_block_head_dims": (32, 64, 128),
+        "fixed_block_dtypes": (torch.bfloat16, torch.float16, torch.float32),
+    }
+
+
+def clear_compile_cache() -> None:
+    """No run-time compilation happens; kept for API compatibility."""
+
+
+class _NativeNamespace:
+    """The reference's pybind module surface (bindings.cpp:34-83) on HIP kernels."""
+
+    @staticmethod
+    def build_info() -> dict[str, object]:
+        return build_info()
+
+    @staticmethod
+    def block_stats(q, k, v):
+        return _block_stats(q, k, v, _lib.STATS_MEANS, q.dtype)
+
+    @staticmethod
+    def block_stats_hyd(q, k, v):
+        return _block_stats(q, k, v, _lib.STATS_HYD, q.dtype)
+
+    @staticmethod
+    def pack_spatial_qkv(q, k, v):
+        batch, heads, tokens, head_dim = q.shape
+        packed = [torch.empty((batch * heads, tokens, head_dim), dtype=q.dtype, device=q.device) for _ in range(3)]
+        side = math.isqrt(tokens)
+        with torch.cuda.device(q.device):
+            check(
+                LIB.pisa_hip_pack_spatial_qkv(
+                    dtype_code(q.dtype), batch, heads, tokens, head_dim, view4(q), view4(k), view4(v),
+                    grid(1, side, side), packed[0].data_ptr(), packed[1].data_ptr(), packed[2].data_ptr(),
+                    stream_of(q.device),
+                ),
+                "pisa_hip_pack_spatial_qkv",
+            )
+        return tuple(packed)
+
+    @staticmethod
+    def unpack_spatial_output(output, batch, heads):
+        bh, tokens, head_dim = output.shape
+        out = output.new_empty((batch, tokens, heads * head_dim))
+        side = math.isqrt(tokens)
+        with torch.cuda.device(output.device):
+            check(
+                LIB.pisa_hip_unpack_spatial_output(
+                    dtype_code(output.dtype), batch, heads, tokens, head_dim, output.contiguous().data_ptr(),
+                    grid(1, side, side), out.data_ptr(), stream_of(output.device),
+                ),
+                "pisa_hip_unpack_spatial_output",
+            )
+        return out
+
+    @staticmethod
+    def fuse_spatial_epilogue(exact_output, exact_lse, approximate_output, approximate_lse, correction, batch, heads):
+        bh, tokens, head_dim = exact_output.shape
+        out = exact_output.new_empty((batch, tokens, heads * head_dim))
+        side = math.isqrt(tokens)
+        with torch.cuda.device(exact_output.device):
+            check(
+                LIB.pisa_hip_fuse_spatial_epilogue(
+                    dtype_code(exact_output.dtype), batch, heads, tokens, head_dim,
+                    exact_output.contiguous().data_ptr(), exact_lse.contiguous().data_ptr(),
+                    approximate_output.contiguous().data_ptr(), approximate_lse.contiguous().data_ptr(),
+                    correction.contiguous().data_ptr(), grid(1, side, side), out.data_ptr(), stream_of(exact_output.device),
+                ),
+                "pisa_hip_fuse_spatial_epilogue",
+            )
+        return out
+
+
+_C = _NativeNamespace()
+
+__all__ = [
+    "BLOCK_SIZE",
+    "HEAD_DIM",
+    "MAX_BLOCKS",
+    "SPATIAL_SPARSE_EXACT_BLOCKS",
+    "SPATIAL_TOKENS",
+    "block_stats_hyd",
+    "build_info",
+    "capabilities",
+    "clear_compile_cache",
+    "dense_attention",
+    "fixed_block_attention",
+    "forward",
+    "forward_spatial_bhtd",
+    "forward_with_routing",
+    "generic_forward",
+    "prepare",
+    "route_topk",
+]
