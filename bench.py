@@ -1,0 +1,210 @@
+#!/usr/bin/env python3
+"""Benchmark of the headline workload on one MI355X.
+
+Workload (BASELINE.json metric, configs[3]): Anima PISA HYD spatial
+self-attention, bf16, B=2 H=16 T=9216 (96x96 raster tokens) D=128, 144
+blocks of 64 tokens, 23 exact blocks per query block.  Inputs are a seeded
+low-frequency Gaussian random field plus 0.3 N(0,1) noise, already resident
+in HBM as BHTD views of [B, T, H, D] storage; one step is one complete
+``mi355x_pisa.forward_spatial_bhtd`` call (statistics, routing, exact tiles,
+tail, first-order correction, merge, raster output).
+
+Also measured in the same process:
+  * the fused attention kernel alone (PisaPlan.attend, one launch), timed
+    with HIP events on the stream it runs on -> roofline against dense bf16
+    MFMA peak;
+  * the dense exact attention kernel of this library on the same shape (the
+    1.8x comparator of the north star);
+  * the CPU oracle (oracle.pisa.hyd_forward) on a bounded sample of heads,
+    scaled to one call -> cpu_baseline.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+Prints one JSON line.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import pathlib
+import statistics
+import sys
+import time
+
+REPO = pathlib.Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO / "comfyui-rdna35-attention_amd"))
+
+BATCH, HEADS, SIDE, HEAD_DIM = 2, 16, 96, 128
+TOKENS = SIDE * SIDE
+BLOCK = 64
+BLOCKS = TOKENS // BLOCK
+EXACT = 23
+PEAK_BF16_FLOPS = 2.5e15  # MI355X dense bf16 MFMA (no sparsity)
+PEAK_HBM_BYTES = 8.0e12
+BASELINE_MS = 25.121  # reference, gfx1151
+METRIC = "PISA call ms + MFMA util %, bf16 B=2 H=16 T=9216 D=128, 23/144 blocks"
+
+
+def algorithmic_flops() -> dict:
+    """Algorithmic FLOP per call, per stage (multiply-add = 2 FLOP)."""
+    bh = BATCH * HEADS
+    exact = bh * BLOCKS * EXACT * 4 * BLOCK * BLOCK * HEAD_DIM          # QK^T + PV on selected blocks
+    tail = bh * BLOCKS * (BLOCKS - EXACT) * 4 * BLOCK * HEAD_DIM        # q . k_bar and P v_bar, unselected
+    correction = bh * TOKENS * 2 * HEAD_DIM * HEAD_DIM                  # q . H_sum
+    stats = bh * BLOCKS * 2 * BLOCK * HEAD_DIM * HEAD_DIM               # H_b per block
+    routing = bh * BLOCKS * BLOCKS * 2 * HEAD_DIM
+    return {"exact": exact, "tail": tail, "correction": correction, "stats": stats, "routing": routing}
+
+
+def time_gpu(fn, steps: int, warmup: int) -> float:
+    """Mean ms per call of `fn` over `steps` calls, HIP events on the current stream."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def blas_threads() -> int:
+    try:
+        from threadpoolctl import threadpool_info
+
+        counts = [pool.get("num_threads", 1) for pool in threadpool_info() if pool.get("user_api") == "blas"]
+        if counts:
+            return int(max(counts))
+    except Exception:
+        pass
+    return os.cpu_count() or 1
+
+
+def cpu_baseline(q, k, v, sample_heads: int) -> dict:
+    """Oracle (numpy) HYD forward on `sample_heads` of the 32 (b, h) heads, scaled to a full call."""
+    sys.path.insert(0, str(REPO))
+    from oracle import layout as olayout
+    from oracle import pisa as opisa
+
+    order = olayout.tile_order(1, SIDE, SIDE)
+    heads = []
+    for tensor in (q, k, v):
+        flat = tensor.detach().float().cpu().numpy().reshape(BATCH * HEADS, TOKENS, HEAD_DIM)[:sample_heads]
+        heads.append(olayout.pack(flat, order))
+    opisa.hyd_forward(*(x[:1] for x in heads), EXACT)  # warm-up (one head)
+    samples = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        opisa.hyd_forward(*heads, EXACT)
+        samples.append((time.perf_counter() - t0) * 1e3)
+    per_call = statistics.median(samples) * (BATCH * HEADS) / sample_heads
+    return {
+        "value": round(per_call, 1),
+        "unit": "ms",
+        "cores": blas_threads(),
+        "kind": "port",
+        "sample": (f"oracle.pisa.hyd_forward (numpy float64) on {sample_heads} of {BATCH * HEADS} heads, "
+                   f"median of 3 after 1 warm-up, scaled x{BATCH * HEADS / sample_heads:g} to one call"),
+    }
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=20)
+    parser.add_argument("--warmup", type=int, default=5)
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--cpu-sample-heads", type=int, default=2)
+    args = parser.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the path shards by (batch, head) "
+              f"with no communication, so N GPUs run N independent shares.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    import mi355x_pisa
+    from mi355x_pisa.synthetic import anima_qkv
+
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    q, k, v = anima_qkv(batch=BATCH, heads=HEADS, side=SIDE, head_dim=HEAD_DIM, seed=0, device=device)
+    scale = 1.0 / math.sqrt(HEAD_DIM)
+
+    # first call (no compilation happens; reported separately as the reference does)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    out = mi355x_pisa.forward_spatial_bhtd(q, k, v, exact_blocks=EXACT)
+    torch.cuda.synchronize()
+    first_call_ms = (time.perf_counter() - t0) * 1e3
+    if not torch.isfinite(out).all():
+        raise RuntimeError("non-finite PISA output")
+
+    # whole call: the metric
+    call_ms = time_gpu(lambda: mi355x_pisa.forward_spatial_bhtd(q, k, v, exact_blocks=EXACT), args.steps, args.warmup)
+
+    # stages on the same inputs: prepare (stats, reduction, routing) and attend (one kernel)
+    out4 = torch.empty((BATCH, TOKENS, HEADS * HEAD_DIM), dtype=q.dtype, device=device)
+    out4 = out4.view(BATCH, TOKENS, HEADS, HEAD_DIM).permute(0, 2, 1, 3)
+    plan = mi355x_pisa.PisaPlan(q, k, v, out4, EXACT, scale, token_grid=(1, SIDE, SIDE))
+    prepare_ms = time_gpu(plan.prepare, args.steps, args.warmup)
+    attend_ms = time_gpu(plan.attend, args.steps, args.warmup)
+    torch.testing.assert_close(out4.permute(0, 2, 1, 3).reshape(BATCH, TOKENS, -1), out, atol=0, rtol=0)
+
+    # dense exact attention of this library on the same shape
+    dense_ms = time_gpu(lambda: mi355x_pisa.dense_attention(q, k, v, scale, merged_output=True), args.steps,
+                        max(1, args.warmup // 2))
+
+    flops = algorithmic_flops()
+    attend_flops = flops["exact"] + flops["tail"] + flops["correction"]
+    achieved = attend_flops / (attend_ms * 1e-3)
+    dense_flops = BATCH * HEADS * 4 * TOKENS * TOKENS * HEAD_DIM
+    total_flops = sum(flops.values())
+    result = {
+        "metric": METRIC,
+        "value": round(call_ms, 4),
+        "unit": "ms",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(call_ms, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": round(call_ms / BASELINE_MS, 5),
+        "dtype": "bf16",
+        "data": "synthetic: seeded 2-D Gaussian random field (sigma 8 tokens) + 0.3*N(0,1) per (b,h,channel)",
+        "config": {"workload": "anima_pisa_hyd_spatial", "batch": BATCH, "heads": HEADS, "tokens": TOKENS,
+                   "grid": [1, SIDE, SIDE], "head_dim": HEAD_DIM, "blocks": BLOCKS, "exact_blocks": EXACT},
+        "roofline": {
+            "bound": "mfma",
+            "kernel": "attention_kernel (exact tiles + tail + first-order + merge)",
+            "achieved": round(achieved / 1e12, 2),
+            "peak": PEAK_BF16_FLOPS / 1e12,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_BF16_FLOPS, 4),
+            "traffic": None,
+        },
+        "mfma_util_pct": round(100 * achieved / PEAK_BF16_FLOPS, 2),
+        "exact_tile_tflops": round(flops["exact"] / (attend_ms * 1e-3) / 1e12, 2),
+        "call_effective_tflops": round(total_flops / (call_ms * 1e-3) / 1e12, 2),
+        "stages_ms": {"prepare": round(prepare_ms, 4), "attend": round(attend_ms, 4)},
+        "first_call_ms": round(first_call_ms, 3),
+        "dense_ms": round(dense_ms, 4),
+        "dense_tflops": round(dense_flops / (dense_ms * 1e-3) / 1e12, 2),
+        "speedup_vs_dense": round(dense_ms / call_ms, 3),
+        "baseline_ms_gfx1151": BASELINE_MS,
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(q, k, v, args.cpu_sample_heads)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

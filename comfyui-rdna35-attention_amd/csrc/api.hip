@@ -224,11 +224,16 @@ int64_t pisa_hip_forward_workspace_bytes(int32_t batch, int32_t heads, int32_t t
     return carve_forward(nullptr, batch * heads, tokens, head_dim, exact_blocks, 2).total;
 }
 
-int pisa_hip_forward(int32_t dtype, int32_t batch, int32_t heads, int32_t tokens, int32_t head_dim, pisa_view q,
-                     pisa_view k, pisa_view v, pisa_view out, pisa_token_grid grid, int32_t exact_blocks, float scale,
-                     int32_t sink_block, int32_t stats_mode, int32_t route_mode, int32_t first_order,
-                     int32_t* debug_indices, float* debug_scores, void* workspace, int64_t workspace_bytes,
-                     void* stream) {
+}  // extern "C"
+
+namespace pisa_host {
+
+// Validation shared by the three PISA entry points; fills the plan on success.
+static int validate_forward(int32_t dtype, int32_t batch, int32_t heads, int32_t tokens, int32_t head_dim,
+                            const pisa_view& q, const pisa_view& k, const pisa_view& v, const pisa_view& out,
+                            const pisa_token_grid& grid, int32_t exact_blocks, float scale, int32_t sink_block,
+                            int32_t stats_mode, int32_t route_mode, void* workspace, int64_t workspace_bytes,
+                            StatsPlan* plan) {
     if (!valid_dtype(dtype)) return fail(PISA_ERR_UNSUPPORTED, "PISA forward supports bf16 and fp16 only");
     if (batch <= 0 || heads <= 0 || tokens <= 0)
         return fail(PISA_ERR_INVALID_ARGUMENT, "PISA forward requires B>0, H>0, T>0");
@@ -260,16 +265,21 @@ int pisa_hip_forward(int32_t dtype, int32_t batch, int32_t heads, int32_t tokens
         return fail(PISA_ERR_WORKSPACE, "workspace of %lld bytes (16-byte aligned) required, got %lld",
                     (long long)need.total, (long long)workspace_bytes);
     if ((rc = check_device())) return rc;
+    *plan = p;
+    return PISA_OK;
+}
 
-    hipStream_t st = static_cast<hipStream_t>(stream);
+static int prepare_impl(int32_t dtype, int32_t heads, int32_t tokens, int32_t head_dim, const pisa_view& q,
+                        const pisa_view& k, const pisa_view& v, const pisa_token_grid& grid, int32_t exact_blocks,
+                        float scale, int32_t sink_block, int32_t stats_mode, int32_t route_mode, int32_t first_order,
+                        int32_t* debug_indices, float* debug_scores, void* workspace, const StatsPlan& p, int bh,
+                        hipStream_t st) {
     const ForwardBuffers w = carve_forward(workspace, bh, tokens, head_dim, exact_blocks, 2);
-    const pisa::TokenMap map = pisa::make_token_map(grid);
-
     pisa::StatsArgs sa;
     sa.q = to_view(q, heads);
     sa.k = to_view(k, heads);
     sa.v = to_view(v, heads);
-    sa.map = map;
+    sa.map = pisa::make_token_map(grid);
     sa.tokens = tokens;
     sa.blocks = p.blocks;
     sa.chunk_blocks = p.chunk_blocks;
@@ -286,6 +296,7 @@ int pisa_hip_forward(int32_t dtype, int32_t batch, int32_t heads, int32_t tokens
     sa.kbar_pad = w.kbar_pad;
     sa.vbar_t_pad = w.vbar_t_pad;
     sa.npad = p.npad;
+    int rc;
     if ((rc = pisa::launch_stats(dtype, stats_mode, sa, bh, st))) return rc;
 
     pisa::ReduceArgs ra;
@@ -320,7 +331,14 @@ int pisa_hip_forward(int32_t dtype, int32_t batch, int32_t heads, int32_t tokens
             hipSuccess)
             return fail(PISA_ERR_LAUNCH, "copy of debug indices failed");
     }
+    return PISA_OK;
+}
 
+static int attend_impl(int32_t dtype, int32_t heads, int32_t tokens, int32_t head_dim, const pisa_view& q,
+                       const pisa_view& k, const pisa_view& out, const pisa_token_grid& grid, int32_t exact_blocks,
+                       float scale, int32_t first_order, void* workspace, const StatsPlan& p, int bh, hipStream_t st) {
+    const ForwardBuffers w = carve_forward(workspace, bh, tokens, head_dim, exact_blocks, 2);
+    const pisa::TokenMap map = pisa::make_token_map(grid);
     pisa::AttnArgs aa;
     aa.q = to_view(q, heads);
     aa.k = to_view(k, heads);
@@ -346,6 +364,53 @@ int pisa_hip_forward(int32_t dtype, int32_t batch, int32_t heads, int32_t tokens
     aa.ht = first_order ? static_cast<const char*>(w.ht) : nullptr;
     aa.corr_scale = scale / static_cast<float>(tokens);
     return pisa::launch_attention(dtype, head_dim, true, true, aa, bh, st);
+}
+
+}  // namespace pisa_host
+
+extern "C" {
+
+int pisa_hip_forward(int32_t dtype, int32_t batch, int32_t heads, int32_t tokens, int32_t head_dim, pisa_view q,
+                     pisa_view k, pisa_view v, pisa_view out, pisa_token_grid grid, int32_t exact_blocks, float scale,
+                     int32_t sink_block, int32_t stats_mode, int32_t route_mode, int32_t first_order,
+                     int32_t* debug_indices, float* debug_scores, void* workspace, int64_t workspace_bytes,
+                     void* stream) {
+    StatsPlan p;
+    int rc = validate_forward(dtype, batch, heads, tokens, head_dim, q, k, v, out, grid, exact_blocks, scale,
+                              sink_block, stats_mode, route_mode, workspace, workspace_bytes, &p);
+    if (rc) return rc;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const int bh = batch * heads;
+    if ((rc = prepare_impl(dtype, heads, tokens, head_dim, q, k, v, grid, exact_blocks, scale, sink_block, stats_mode,
+                           route_mode, first_order, debug_indices, debug_scores, workspace, p, bh, st)))
+        return rc;
+    return attend_impl(dtype, heads, tokens, head_dim, q, k, out, grid, exact_blocks, scale, first_order, workspace, p,
+                       bh, st);
+}
+
+int pisa_hip_prepare(int32_t dtype, int32_t batch, int32_t heads, int32_t tokens, int32_t head_dim, pisa_view q,
+                     pisa_view k, pisa_view v, pisa_view out, pisa_token_grid grid, int32_t exact_blocks, float scale,
+                     int32_t sink_block, int32_t stats_mode, int32_t route_mode, int32_t first_order,
+                     void* workspace, int64_t workspace_bytes, void* stream) {
+    StatsPlan p;
+    int rc = validate_forward(dtype, batch, heads, tokens, head_dim, q, k, v, out, grid, exact_blocks, scale,
+                              sink_block, stats_mode, route_mode, workspace, workspace_bytes, &p);
+    if (rc) return rc;
+    return prepare_impl(dtype, heads, tokens, head_dim, q, k, v, grid, exact_blocks, scale, sink_block, stats_mode,
+                        route_mode, first_order, nullptr, nullptr, workspace, p, batch * heads,
+                        static_cast<hipStream_t>(stream));
+}
+
+int pisa_hip_attend(int32_t dtype, int32_t batch, int32_t heads, int32_t tokens, int32_t head_dim, pisa_view q,
+                    pisa_view k, pisa_view v, pisa_view out, pisa_token_grid grid, int32_t exact_blocks, float scale,
+                    int32_t sink_block, int32_t stats_mode, int32_t route_mode, int32_t first_order,
+                    void* workspace, int64_t workspace_bytes, void* stream) {
+    StatsPlan p;
+    int rc = validate_forward(dtype, batch, heads, tokens, head_dim, q, k, v, out, grid, exact_blocks, scale,
+                              sink_block, stats_mode, route_mode, workspace, workspace_bytes, &p);
+    if (rc) return rc;
+    return attend_impl(dtype, heads, tokens, head_dim, q, k, out, grid, exact_blocks, scale, first_order, workspace, p,
+                       batch * heads, static_cast<hipStream_t>(stream));
 }
 
 int64_t pisa_hip_block_stats_workspace_bytes(int32_t batch, int32_t heads, int32_t tokens, int32_t head_dim) {

@@ -235,7 +235,7 @@ def _block_stats_hyd_op_fake(q, k, v):
 
 @torch.library.custom_op("mi355x_pisa::generic_forward", mutates_args=(), device_types="cuda")
 def _generic_forward_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, exact_blocks: int, scale: float,
-                        first_order: bool, frames: int, height: int, width: int) -> torch.Tensor:
+                        first_order: bool, sink_block: int, frames: int, height: int, width: int) -> torch.Tensor:
     batch, heads, tokens, head_dim = q.shape
     out = q.new_empty((batch, tokens, heads, head_dim))
     out4 = out.permute(0, 2, 1, 3)
@@ -243,14 +243,14 @@ def _generic_forward_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, exact
     if exact_blocks == blocks:
         _launch_dense(q, k, v, out4, scale)
     else:
-        _launch_pisa(q, k, v, out4, grid(frames, height, width), exact_blocks, scale, -2,
+        _launch_pisa(q, k, v, out4, grid(frames, height, width), exact_blocks, scale, sink_block,
                      _lib.STATS_GENERIC, _lib.ROUTE_CENTROID, first_order)
     return out
 
 
 @_generic_forward_op.register_fake
-def _generic_forward_op_fake(q, k, v, exact_blocks, scale, first_order, frames, height, width):
-    del k, v, exact_blocks, scale, first_order, frames, height, width
+def _generic_forward_op_fake(q, k, v, exact_blocks, scale, first_order, sink_block, frames, height, width):
+    del k, v, exact_blocks, scale, first_order, sink_block, frames, height, width
     return q.new_empty((q.shape[0], q.shape[2], q.shape[1], q.shape[3]))
 
 
@@ -376,7 +376,8 @@ def forward_spatial_bhtd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, exac
 
 
 def generic_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, exact_blocks: int, scale: float,
-                    first_order: bool, token_grid: tuple[int, int, int] | None = None) -> torch.Tensor:
+                    first_order: bool, token_grid: tuple[int, int, int] | None = None,
+                    sink_block: int | None = None) -> torch.Tensor:
     """Generic PISA over [B,H,T,D] views (generic_pisa.py:141-232 semantics).
 
     Centroid routing without the HYD bias, dtype-rounded centred keys for
@@ -384,8 +385,10 @@ def generic_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, exact_blo
     selects per-frame 8x8 tile blocks; the output is [B,T,H,D] contiguous.
     """
     frames, height, width = token_grid if token_grid is not None else (0, 0, 0)
-    return _generic_forward_op(q, k, v, int(exact_blocks), float(scale), bool(first_order),
-                               int(frames), int(height), int(width))
+    blocks = (q.shape[2] + BLOCK_SIZE - 1) // BLOCK_SIZE
+    _check_exact_and_sink(exact_blocks, blocks, sink_block)
+    return _generic_forward_op(q, k, v, int(exact_blocks), _float32(scale), bool(first_order),
+                               -2 if sink_block is None else int(sink_block), int(frames), int(height), int(width))
 
 
 def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float,
@@ -445,6 +448,53 @@ def forward_with_routing(q4: torch.Tensor, k4: torch.Tensor, v4: torch.Tensor, e
                  _lib.STATS_HYD if hyd else _lib.STATS_GENERIC, _lib.ROUTE_HYD if hyd else _lib.ROUTE_CENTROID,
                  first_order, debug_indices=indices, debug_scores=scores)
     return out, scores, indices[..., :exact_blocks]
+
+
+class PisaPlan:
+    """One sparse PISA problem bound to its workspace, run as two stages.
+
+    ``prepare()`` enqueues the statistics, H_sum reduction and routing
+    kernels, ``attend()`` the fused exact/tail/correction/merge kernel that
+    reads the prepared workspace; ``forward()`` runs both and equals
+    ``forward_spatial_bhtd`` / ``generic_forward`` on the same arguments.
+    q4/k4/v4/out4 are [B,H,T,D] views; they must stay alive and unchanged
+    between prepare() and attend().
+    """
+
+    def __init__(self, q4, k4, v4, out4, exact_blocks: int, scale: float | None = None,
+                 sink_block: int | None = None, hyd: bool = True, first_order: bool = True,
+                 token_grid: tuple[int, int, int] | None = None):
+        batch, heads, tokens, head_dim = q4.shape
+        self.tensors = (q4, k4, v4, out4)
+        self.shape = (batch, heads, tokens, head_dim)
+        self.exact_blocks = int(exact_blocks)
+        self.scale = _float32(1.0 / math.sqrt(head_dim) if scale is None else scale)
+        self.sink_block = -2 if sink_block is None else int(sink_block)
+        self.modes = (_lib.STATS_HYD, _lib.ROUTE_HYD) if hyd else (_lib.STATS_GENERIC, _lib.ROUTE_CENTROID)
+        self.first_order = int(bool(first_order))
+        self.grid = grid(*(token_grid or (0, 0, 0)))
+        self.device = q4.device
+        self.workspace_bytes = LIB.pisa_hip_forward_workspace_bytes(batch, heads, tokens, head_dim, self.exact_blocks)
+        self.workspace = torch.empty(self.workspace_bytes, dtype=torch.uint8, device=self.device)
+
+    def _args(self):
+        q4, k4, v4, out4 = self.tensors
+        return (dtype_code(q4.dtype), *self.shape, view4(q4), view4(k4), view4(v4), view4(out4), self.grid,
+                self.exact_blocks, self.scale, self.sink_block, *self.modes, self.first_order,
+                self.workspace.data_ptr(), self.workspace_bytes, stream_of(self.device))
+
+    def prepare(self) -> None:
+        with torch.cuda.device(self.device):
+            check(LIB.pisa_hip_prepare(*self._args()), "pisa_hip_prepare")
+
+    def attend(self) -> torch.Tensor:
+        with torch.cuda.device(self.device):
+            check(LIB.pisa_hip_attend(*self._args()), "pisa_hip_attend")
+        return self.tensors[3]
+
+    def forward(self) -> torch.Tensor:
+        self.prepare()
+        return self.attend()
 
 
 def prepare(device_index: int | None = None) -> None:
@@ -578,6 +628,7 @@ __all__ = [
     "forward",
     "forward_spatial_bhtd",
     "forward_with_routing",
+    "PisaPlan",
     "generic_forward",
     "prepare",
     "route_topk",

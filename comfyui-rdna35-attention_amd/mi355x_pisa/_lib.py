@@ -58,6 +58,16 @@ _SIGNATURES = {
         [_i32, _i32, _i32, _i32, _i32, PisaView, PisaView, PisaView, PisaView, PisaTokenGrid,
          _i32, _f32, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _i64, _vp],
     ),
+    "pisa_hip_prepare": (
+        ctypes.c_int,
+        [_i32, _i32, _i32, _i32, _i32, PisaView, PisaView, PisaView, PisaView, PisaTokenGrid,
+         _i32, _f32, _i32, _i32, _i32, _i32, _vp, _i64, _vp],
+    ),
+    "pisa_hip_attend": (
+        ctypes.c_int,
+        [_i32, _i32, _i32, _i32, _i32, PisaView, PisaView, PisaView, PisaView, PisaTokenGrid,
+         _i32, _f32, _i32, _i32, _i32, _i32, _vp, _i64, _vp],
+    ),
     "pisa_hip_block_stats_workspace_bytes": (_i64, [_i32, _i32, _i32, _i32]),
     "pisa_hip_block_stats": (
         ctypes.c_int,

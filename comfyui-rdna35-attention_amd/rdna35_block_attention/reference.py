@@ -1,0 +1,189 @@
+"""Layout normalisation and the eager ("reference" backend) implementations.
+
+Public names and behaviour follow the reference's reference.py:
+normalize_qkv_to_bh_t_d (:38-111), per-block mask slicing (:114-156),
+fixed_block_attention_ref (:159-200), fixed_block_attention_bthd (:203-224),
+block_diagonal_sdpa_mask (:227-241), fixed_block_attention_sdpa (:244-272)
+and full_attention_sdpa_bhtd (:275-293).  These eager versions serve the
+calls the HIP kernels do not take (masks, CPU tensors, unsupported shapes)
+and the explicit ``mode="reference"``; eligible ROCm calls never use them.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Callable
+
+import torch
+
+_LAYOUT_ALIASES = {
+    "auto": "auto",
+    "bhtd": "bhtd",
+    "b,h,t,d": "bhtd",
+    "bh_t_d": "bh_t_d",
+    "bhtd_flat": "bh_t_d",
+    "bhtdflat": "bh_t_d",
+    "bthd": "bthd",
+    "b,t,h*d": "bthd",
+    "b_t_hd": "bthd",
+}
+
+
+@dataclass(frozen=True)
+class LayoutInfo:
+    layout: str
+    batch: int | None
+    heads: int | None
+    tokens: int
+    head_dim: int
+    restore: Callable[[torch.Tensor], torch.Tensor]
+
+
+def _canonical_layout(layout: str) -> str:
+    key = layout.lower().replace("-", "_").replace(" ", "")
+    if key not in _LAYOUT_ALIASES:
+        raise ValueError(f"Unsupported layout '{layout}'.")
+    return _LAYOUT_ALIASES[key]
+
+
+def normalize_qkv_to_bh_t_d(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, layout: str = "auto",
+                            heads: int | None = None):
+    """Flatten q/k/v to contiguous [B*H, T, D]; returns (q, k, v, LayoutInfo with restore())."""
+    if q.shape != k.shape or q.shape != v.shape:
+        raise ValueError(
+            f"Fixed block self-attention requires q/k/v to have identical shapes, got {q.shape}, {k.shape}, {v.shape}.")
+    chosen = _canonical_layout(layout)
+    if chosen == "auto":
+        if q.ndim not in (3, 4):
+            raise ValueError(f"Cannot infer layout for rank-{q.ndim} tensor.")
+        chosen = "bhtd" if q.ndim == 4 else "bh_t_d"
+
+    if chosen == "bhtd":
+        if q.ndim != 4:
+            raise ValueError(f"layout='bhtd' expects [B,H,T,D], got rank {q.ndim}.")
+        b, h, t, d = q.shape
+        flat = [x.contiguous().reshape(b * h, t, d) for x in (q, k, v)]
+        return (*flat, LayoutInfo(chosen, b, h, t, d, lambda out: out.reshape(b, h, t, d)))
+
+    if chosen == "bh_t_d":
+        if q.ndim != 3:
+            raise ValueError(f"layout='bh_t_d' expects [BH,T,D], got rank {q.ndim}.")
+        bh, t, d = q.shape
+        return (q.contiguous(), k.contiguous(), v.contiguous(),
+                LayoutInfo(chosen, None, None, t, d, lambda out: out.reshape(bh, t, d)))
+
+    if q.ndim != 3:
+        raise ValueError(f"layout='bthd' expects [B,T,H*D], got rank {q.ndim}.")
+    if heads is None or heads <= 0:
+        raise ValueError("layout='bthd' requires a positive heads argument.")
+    b, t, channels = q.shape
+    if channels % heads:
+        raise ValueError(f"channels={channels} is not divisible by heads={heads}.")
+    d = channels // heads
+
+    def to_flat(x: torch.Tensor) -> torch.Tensor:
+        return x.reshape(b, t, heads, d).transpose(1, 2).contiguous().reshape(b * heads, t, d)
+
+    def restore(out: torch.Tensor) -> torch.Tensor:
+        return out.reshape(b, heads, t, d).transpose(1, 2).contiguous().reshape(b, t, channels)
+
+    return (to_flat(q), to_flat(k), to_flat(v), LayoutInfo(chosen, b, heads, t, d, restore))
+
+
+def _mask_block(mask: torch.Tensor | None, start: int, end: int, *, batch_heads: int, info: LayoutInfo,
+                device: torch.device) -> torch.Tensor | None:
+    """The [BH, n, n] slice of a 2-D/3-D/4-D attention mask for tokens [start, end)."""
+    if mask is None:
+        return None
+    m = mask.to(device=device)
+    square = (info.tokens, info.tokens)
+    n = end - start
+    if m.ndim == 2:
+        if tuple(m.shape[-2:]) != square:
+            raise ValueError(f"2D mask must have shape [T,T], got {tuple(m.shape)}.")
+        return m[start:end, start:end].unsqueeze(0).expand(batch_heads, n, n)
+    if m.ndim == 3:
+        if tuple(m.shape[-2:]) != square:
+            raise ValueError(f"3D mask must end with [T,T], got {tuple(m.shape)}.")
+        part = m[:, start:end, start:end]
+        lead = part.shape[0]
+        if info.batch is not None and lead == info.batch:
+            return part.repeat_interleave(info.heads, dim=0)
+        if lead == 1:
+            return part.expand(batch_heads, n, n)
+        if lead == batch_heads:
+            return part
+        raise ValueError(f"3D mask batch dimension {lead} is not compatible with BH={batch_heads}.")
+    if m.ndim == 4:
+        if info.batch is None or info.heads is None:
+            raise ValueError("4D mask requires a layout with known B and H.")
+        if tuple(m.shape[-2:]) != square:
+            raise ValueError(f"4D mask must end with [T,T], got {tuple(m.shape)}.")
+        if m.shape[0] not in (1, info.batch):
+            raise ValueError(f"4D mask batch dimension {m.shape[0]} is not compatible with B={info.batch}.")
+        if m.shape[1] not in (1, info.heads):
+            raise ValueError(f"4D mask head dimension {m.shape[1]} is not compatible with H={info.heads}.")
+        full = m.expand(info.batch, info.heads, info.tokens, info.tokens)
+        return full[:, :, start:end, start:end].reshape(batch_heads, n, n)
+    raise ValueError(f"Unsupported mask rank {m.ndim}.")
+
+
+def fixed_block_attention_ref(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, block_size: int = 64,
+                              scale: float | None = None, causal: bool = False, layout: str = "auto", *,
+                              heads: int | None = None, mask: torch.Tensor | None = None) -> torch.Tensor:
+    """Eager fixed block-diagonal attention: every block of `block_size` tokens attends to itself (fp32 math)."""
+    qf, kf, vf, info = normalize_qkv_to_bh_t_d(q, k, v, layout=layout, heads=heads)
+    if block_size <= 0:
+        raise ValueError("block_size must be positive.")
+    bh, tokens, head_dim = qf.shape
+    s = float(scale) if scale is not None else 1.0 / math.sqrt(head_dim)
+    out = torch.empty_like(qf)
+    for start in range(0, tokens, block_size):
+        end = min(start + block_size, tokens)
+        scores = torch.matmul(qf[:, start:end].float(), kf[:, start:end].float().transpose(-2, -1)) * s
+        if causal:
+            upper = torch.ones((end - start, end - start), dtype=torch.bool, device=q.device).triu(1)
+            scores = scores.masked_fill(upper, -torch.inf)
+        block_mask = _mask_block(mask, start, end, batch_heads=bh, info=info, device=q.device)
+        if block_mask is not None:
+            if block_mask.dtype == torch.bool:
+                scores = scores.masked_fill(~block_mask, -torch.inf)
+            else:
+                scores = scores + block_mask.to(scores.dtype)
+        out[:, start:end] = torch.matmul(torch.softmax(scores, dim=-1), vf[:, start:end].float()).to(qf.dtype)
+    return info.restore(out)
+
+
+def fixed_block_attention_bthd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, heads: int, block_size: int = 64,
+                               scale: float | None = None, causal: bool = False, *,
+                               mask: torch.Tensor | None = None) -> torch.Tensor:
+    return fixed_block_attention_ref(q, k, v, block_size=block_size, scale=scale, causal=causal, layout="bthd",
+                                     heads=heads, mask=mask)
+
+
+def block_diagonal_sdpa_mask(tokens: int, *, block_size: int = 64, causal: bool = False,
+                             device: torch.device | None = None) -> torch.Tensor:
+    if block_size <= 0:
+        raise ValueError("block_size must be positive.")
+    pos = torch.arange(tokens, device=device)
+    mask = (pos[:, None] // block_size) == (pos[None, :] // block_size)
+    if causal:
+        mask = mask & (pos[None, :] <= pos[:, None])
+    return mask
+
+
+def fixed_block_attention_sdpa(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, block_size: int = 64,
+                               scale: float | None = None, causal: bool = False, layout: str = "auto", *,
+                               heads: int | None = None) -> torch.Tensor:
+    qf, kf, vf, info = normalize_qkv_to_bh_t_d(q, k, v, layout=layout, heads=heads)
+    mask = block_diagonal_sdpa_mask(info.tokens, block_size=block_size, causal=causal, device=qf.device)
+    extra = {} if scale is None else {"scale": float(scale)}
+    out = torch.nn.functional.scaled_dot_product_attention(qf[:, None], kf[:, None], vf[:, None], attn_mask=mask,
+                                                           dropout_p=0.0, is_causal=False, **extra)[:, 0]
+    return info.restore(out.to(qf.dtype))
+
+
+def full_attention_sdpa_bhtd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, scale: float | None = None,
+                             causal: bool = False) -> torch.Tensor:
+    extra = {} if scale is None else {"scale": float(scale)}
+    return torch.nn.functional.scaled_dot_product_attention(q, k, v, dropout_p=0.0, is_causal=causal, **extra)

@@ -145,6 +145,28 @@ PISA_HIP_EXPORT int pisa_hip_forward(int32_t dtype, int32_t batch, int32_t heads
                      int32_t* debug_indices, float* debug_scores,
                      void* workspace, int64_t workspace_bytes, void* stream);
 
+/*
+ * pisa_hip_forward in two stages sharing one workspace:
+ *   pisa_hip_prepare  statistics, H_sum reduction, routing and top-k (3 launches)
+ *   pisa_hip_attend   exact tiles + tail + correction + merge (1 launch)
+ * attend reads what prepare left in the workspace, so the pair must use the
+ * same arguments and workspace, in that order on one stream; prepare + attend
+ * is exactly pisa_hip_forward.  Callers that re-attend with unchanged
+ * statistics, and profilers that time the attention kernel alone, use these.
+ * The reference computes the same stages inside _forward_impl
+ * (__init__.py:254-298).
+ */
+PISA_HIP_EXPORT int pisa_hip_prepare(int32_t dtype, int32_t batch, int32_t heads, int32_t tokens, int32_t head_dim,
+                     pisa_view q, pisa_view k, pisa_view v, pisa_view out, pisa_token_grid grid,
+                     int32_t exact_blocks, float scale, int32_t sink_block,
+                     int32_t stats_mode, int32_t route_mode, int32_t first_order,
+                     void* workspace, int64_t workspace_bytes, void* stream);
+PISA_HIP_EXPORT int pisa_hip_attend(int32_t dtype, int32_t batch, int32_t heads, int32_t tokens, int32_t head_dim,
+                    pisa_view q, pisa_view k, pisa_view v, pisa_view out, pisa_token_grid grid,
+                    int32_t exact_blocks, float scale, int32_t sink_block,
+                    int32_t stats_mode, int32_t route_mode, int32_t first_order,
+                    void* workspace, int64_t workspace_bytes, void* stream);
+
 /* ---- subsystem 1: block statistics ------------------------------------- */
 
 PISA_HIP_EXPORT int64_t pisa_hip_block_stats_workspace_bytes(int32_t batch, int32_t heads, int32_t tokens,

@@ -1,0 +1,107 @@
+"""The C ABI library loads on the CPU and exports exactly what include/pisa_hip.h declares.
+
+No kernel is launched here: only metadata calls and argument validation that
+returns before touching a device.
+"""
+from __future__ import annotations
+
+import ctypes
+import pathlib
+import re
+import subprocess
+
+import pytest
+
+REPO = pathlib.Path(__file__).resolve().parents[1]
+HEADER = REPO / "include" / "pisa_hip.h"
+
+
+def _declared() -> set[str]:
+    text = HEADER.read_text()
+    return set(re.findall(r"PISA_HIP_EXPORT\s+[\w\s\*]+?\b((?:pisa|attn)_hip_\w+)\s*\(", text))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from mi355x_pisa import _lib
+
+    return _lib
+
+
+def test_header_declares_the_api():
+    names = _declared()
+    assert {"pisa_hip_forward", "pisa_hip_prepare", "pisa_hip_attend", "pisa_hip_block_stats",
+            "pisa_hip_route_topk", "attn_hip_dense_forward", "attn_hip_fixed_block_forward",
+            "pisa_hip_pack_spatial_qkv", "pisa_hip_unpack_spatial_output",
+            "pisa_hip_fuse_spatial_epilogue"} <= names
+
+
+def test_library_exports_every_declared_symbol(lib):
+    out = subprocess.run(["nm", "-D", "--defined-only", str(lib.LIB_PATH)], capture_output=True, text=True,
+                         check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
+    declared = _declared()
+    assert declared == exported, (declared ^ exported)
+    assert declared == set(lib.EXPORTED_SYMBOLS)
+    for name in declared:
+        assert hasattr(lib.LIB, name)
+
+
+def test_metadata_calls(lib):
+    assert lib.LIB.pisa_hip_api_version() == 1
+    info = lib.build_info_string()
+    assert "architecture=gfx950" in info and "block_size=64" in info
+    assert lib.LIB.pisa_hip_status_string(0) == b"ok"
+    assert lib.LIB.pisa_hip_status_string(3) == b"workspace too small"
+    small = ctypes.create_string_buffer(4)
+    assert lib.LIB.pisa_hip_build_info(small, 4) == 1
+
+
+def test_workspace_sizes(lib):
+    c4 = lib.LIB.pisa_hip_forward_workspace_bytes(2, 16, 9216, 128, 23)
+    # transposed V blocks alone are B*H*T*D bf16
+    assert c4 > 2 * 16 * 9216 * 128 * 2
+    assert lib.LIB.pisa_hip_forward_workspace_bytes(0, 16, 9216, 128, 23) == 0
+    assert lib.LIB.attn_hip_dense_workspace_bytes(2, 16, 512, 128) == 2 * 16 * 512 * 128 * 2
+    assert lib.LIB.attn_hip_dense_workspace_bytes(1, 1, 65, 64) == 128 * 64 * 2
+
+
+def _views(lib):
+    fake = lib.PisaView(0x1000, 9216 * 16 * 128, 128, 16 * 128)
+    return fake, fake, fake, fake
+
+
+def test_forward_validation_rejects_before_any_launch(lib):
+    q, k, v, o = _views(lib)
+    grid = lib.grid(1, 96, 96)
+    args = dict(dtype=0, batch=2, heads=16, tokens=9216, head_dim=128, exact=23, scale=0.088, sink=-2, stats=1,
+                route=0, first=1)
+
+    def call(**over):
+        a = {**args, **over}
+        return lib.LIB.pisa_hip_forward(a["dtype"], a["batch"], a["heads"], a["tokens"], a["head_dim"], q, k, v, o,
+                                        over.get("grid", grid), a["exact"], a["scale"], a["sink"], a["stats"],
+                                        a["route"], a["first"], None, None, None, 0, None)
+
+    assert call(head_dim=64) == 2                      # unsupported head_dim
+    assert call(dtype=2) == 2                          # fp32 not supported by PISA
+    assert call(exact=144) == 1                        # dense goes to attn_hip_dense_forward
+    assert call(exact=0, sink=0) == 1                  # sink needs an exact block
+    assert call(scale=0.0) == 1
+    assert call(scale=float("inf")) == 1
+    assert call(grid=lib.grid(1, 96, 90)) == 1         # width not a multiple of 8
+    assert call(grid=lib.grid(2, 96, 96)) == 1         # grid does not match T
+    assert call() == 3                                 # no workspace
+    assert b"workspace" in lib.LIB.pisa_hip_last_error()
+
+
+def test_other_entry_points_validate(lib):
+    q, k, v, o = _views(lib)
+    assert lib.LIB.attn_hip_dense_forward(0, 1, 1, 64, 64, 96, q, k, v, o, 0.1, None, 0, None) == 2
+    assert lib.LIB.attn_hip_fixed_block_forward(0, 1, 1, 64, 48, 64, q, k, v, o, 0.1, 0, None) == 2
+    assert lib.LIB.attn_hip_fixed_block_forward(0, 1, 1, 64, 64, 32, q, k, v, o, 0.1, 0, None) == 2
+    assert lib.LIB.pisa_hip_route_topk(1, 2000, 128, None, None, None, 1, 0.1, -2, 3, None, None, None) == 2
+    assert lib.LIB.pisa_hip_route_topk(1, 10, 128, None, None, None, 1, 0.1, 5, 3, None, None, None) == 1
+    misaligned = lib.PisaView(0x1002, 0, 0, 128)
+    assert lib.LIB.pisa_hip_pack_spatial_qkv(0, 1, 1, 9216, 128, misaligned, k, v, lib.grid(1, 96, 96), None,
+                                             None, None, None) == 1

@@ -1,0 +1,134 @@
+"""GPU checks at the full BASELINE configurations.
+
+The oracle cannot run a whole config in seconds, so each config is checked
+by (a) size-independent properties at full size - bit-exact selection
+against the CPU top-k of the kernel's own scores, constant values returned
+exactly, per-block-constant keys reducing PISA to dense attention, strided
+and packed layouts giving identical bits - and (b) oracle comparisons on a
+subset of heads or query rows of the full-size problem.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import assert_close, np32, packed_to_merged, spatial_to_packed
+from oracle import attention as oatt
+from oracle import layout as olayout
+from oracle import pisa as opisa
+
+pytestmark = pytest.mark.gpu
+D = 128
+
+
+@pytest.fixture(scope="module")
+def native():
+    import mi355x_pisa
+
+    return mi355x_pisa
+
+
+@pytest.fixture(scope="module")
+def anima():
+    from mi355x_pisa.synthetic import anima_qkv
+
+    return anima_qkv(batch=2, heads=16, seed=0, device="cuda")
+
+
+def test_c4_selection_bit_exact_and_oracle_heads(native, anima):
+    q, k, v = anima
+    out, scores, idx = native.forward_with_routing(q, k, v, 23, D ** -0.5, token_grid=(1, 96, 96))
+    assert torch.isfinite(out).all()
+    np.testing.assert_array_equal(idx.cpu().numpy(), opisa.topk_ascending(np32(scores), 23))
+    # the spatial entry point gives the same bits
+    spatial = native.forward_spatial_bhtd(q, k, v, exact_blocks=23)
+    assert torch.equal(spatial.view(2, 9216, 16, D).permute(0, 2, 1, 3), out)
+    heads = [(0, 0), (1, 15)]
+    for b, h in heads:
+        packed = [spatial_to_packed(t[b:b + 1, h:h + 1], 1, 96, 96) for t in (q, k, v)]
+        expected, exp_scores, _ = opisa.hyd_forward(*packed, 23, return_selection=True)
+        assert_close(np32(scores[b * 16 + h]), exp_scores[0], 1e-4, 1e-4, "C4 routing scores")
+        merged = packed_to_merged(expected, 1, 1, 1, 96, 96)
+        assert_close(np32(out[b, h]), merged[0], 5e-2, 5e-2, f"C4 head {(b, h)}")
+
+
+def test_c4_constant_values_are_exact(native, anima):
+    q, k, _ = anima
+    v = torch.full_like(q, 0.3125)  # exactly representable; any convex combination returns it
+    out = native.forward_spatial_bhtd(q, k, v, exact_blocks=23)
+    assert torch.equal(out, torch.full_like(out, 0.3125))
+
+
+def test_c4_blockwise_constant_keys_reduce_to_dense(native, anima):
+    q, k, v = anima
+    order = torch.from_numpy(olayout.tile_order(1, 96, 96)).cuda()
+    blocks = k[:, :, order].reshape(2, 16, 144, 64, D)[:, :, :, :1].expand(2, 16, 144, 64, D)
+    k_const = torch.empty_like(k).contiguous()
+    k_const[:, :, order] = blocks.reshape(2, 16, 9216, D)
+    storage = k_const.permute(0, 2, 1, 3).contiguous()
+    k_view = storage.permute(0, 2, 1, 3)
+    sparse = native.forward_spatial_bhtd(q, k_view, v, exact_blocks=23)
+    dense = native.forward_spatial_bhtd(q, k_view, v, exact_blocks=144)
+    torch.testing.assert_close(sparse.float(), dense.float(), atol=5e-2, rtol=5e-2)
+
+
+def test_c2_dense_self_and_cross(native):
+    from mi355x_pisa.synthetic import normal_qkv
+
+    q, k, v = normal_qkv((2, 16, 9216, D), seed=2, scale=0.5, device="cuda")
+    out = native.dense_attention(q, k, v, D ** -0.5)
+    assert torch.isfinite(out).all()
+    rows = slice(0, 256)
+    for b, h in ((0, 0), (1, 9)):
+        expected = oatt.dense_attention(np32(q[b, h, rows]), np32(k[b, h]), np32(v[b, h]))
+        assert_close(np32(out[b, h, rows]), expected, 5e-2, 5e-2, f"C2 head {(b, h)}")
+    ones = torch.full_like(v, -1.5)
+    assert torch.equal(native.dense_attention(q, k, ones, D ** -0.5), ones)
+    kc, vc = (t[:, :, :512].contiguous() for t in (k, v))
+    cross = native.dense_attention(q, kc, vc, D ** -0.5)
+    for b, h in ((0, 3), (1, 15)):
+        expected = oatt.dense_attention(np32(q[b, h, rows]), np32(kc[b, h]), np32(vc[b, h]))
+        assert_close(np32(cross[b, h, rows]), expected, 5e-2, 5e-2, "C2 cross")
+
+
+@pytest.mark.parametrize("tokens", [9170, 16500])
+def test_c3_h3_strided_equals_packed(native, tokens):
+    gen = torch.Generator().manual_seed(tokens)
+    qkv = torch.randn((1, tokens, 3, 56, D), generator=gen).to(torch.bfloat16).cuda()
+    q, k, v = (qkv[:, :, i].permute(0, 2, 1, 3) for i in range(3))
+    v = v.clone()  # the reference benchmark clones V (nodes.py:334-337)
+    strided = native.dense_attention(q, k, v, D ** -0.5, merged_output=True)
+    packed = native.dense_attention(q.contiguous(), k.contiguous(), v.contiguous(), D ** -0.5, merged_output=True)
+    assert torch.equal(strided, packed)
+    rows = slice(tokens - 200, tokens)
+    expected = oatt.dense_attention(np32(q[0, 17, rows]), np32(k[0, 17]), np32(v[0, 17]))
+    got = np32(strided).reshape(tokens, 56, D)[rows, 17]
+    assert_close(got, expected, 5e-2, 5e-2, "C3 head 17")
+
+
+def test_c1_fixed_block_fp32(native):
+    from mi355x_pisa.synthetic import normal_qkv
+
+    q, k, v = normal_qkv((1, 8, 4096, 64), seed=1, dtype=torch.float32, device="cuda")
+    out = native.fixed_block_attention(q, k, v, 1 / 8.0)
+    expected = oatt.fixed_block_attention(np32(q), np32(k), np32(v), scale=1 / 8.0)
+    assert_close(np32(out), expected, 1e-5, 1e-5, "C1")
+
+
+def test_c5_video_selection_and_one_head(native):
+    from mi355x_pisa.synthetic import video_qkv
+
+    grid = (16, 32, 64)
+    q, k, v = video_qkv(batch=1, heads=40, grid=grid, seed=5, device="cuda")
+    exact = math.ceil(0.15625 * 512)
+    out, scores, idx = native.forward_with_routing(q, k, v, exact, D ** -0.5, hyd=False, token_grid=grid)
+    assert torch.isfinite(out).all()
+    np.testing.assert_array_equal(idx.cpu().numpy(), opisa.topk_ascending(np32(scores), exact))
+    merged = native.generic_forward(q, k, v, exact, D ** -0.5, True, token_grid=grid)
+    assert torch.equal(merged.permute(0, 2, 1, 3), out)
+    packed = [spatial_to_packed(t[:, 21:22], *grid) for t in (q, k, v)]
+    expected = packed_to_merged(opisa.generic_forward(*packed, exact, dtype="bf16"), 1, 1, *grid)
+    assert_close(np32(out[0, 21]), expected[0], 5e-2, 5e-2, "C5 head 21")
