@@ -39,6 +39,11 @@ COMMON_FLAGS = [
     "-target-feature",
     "-Xclang",
     "-packed-fp32-ops",
+    # MFMA accumulators in architectural VGPRs: the softmax reads and rescales
+    # them with VALU ops, and the AGPR form costs a v_accvgpr copy per value
+    # (and spills in the attention kernels).
+    "-mllvm",
+    "-amdgpu-mfma-vgpr-form=1",
     f"-I{REPO_ROOT / 'include'}",
 ]
 

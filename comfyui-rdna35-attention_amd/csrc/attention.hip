@@ -29,47 +29,58 @@
 
 namespace pisa {
 
+constexpr float kLazyRescale = 8.0f;  // log2 headroom before the running max is moved
 
+// Online-softmax update of one 64-key chunk held transposed in `s`
+// (s[mt][nt][v] = score of key 32mt + 8(v/4) + 4half + v%4, query 32nt + col).
+// `c` converts raw scores to the log2 domain (c = scale*log2(e) for exact
+// chunks, 1 for tail chunks whose scores are pre-converted).  The running max
+// only moves when a column's chunk max exceeds it by kLazyRescale, so the
+// O rescale (128 accumulators) runs on the first chunk and rarely after;
+// probabilities are then bounded by 2^kLazyRescale, well inside bf16/fp32.
 template <typename T, int D>
-struct Wave {
-    typedef typename Elem<T>::vec8 vec8;
-    static constexpr int KT = D / 16;   // contraction steps over head_dim
-    static constexpr int MD = D / 32;   // 32-row tiles of head_dim
-};
-
-// ---- one 64-key chunk: S^T = K Q^T, online softmax update, O^T += V^T P^T.
-// `s` holds the raw scores on entry.  kind: 0 exact full chunk, 1 exact chunk
-// with key bound, 2 tail chunk.
-template <typename T, int D>
-__device__ __forceinline__ void softmax_update(f32x16 (&s)[2][2], float (&m)[2], float (&l)[2],
-                                               float (&lt)[2], f32x16 (&o)[D / 32][2], bool tail) {
+__device__ __forceinline__ void softmax_update(f32x16 (&s)[2][2], float (&m)[2], float (&l)[2], float (&lt)[2],
+                                               f32x16 (&o)[D / 32][2], float c, bool tail) {
+    float mx[2];
+    bool need[2];
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
-        float mx = -__builtin_inff();
+        float x = -__builtin_inff();
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-            for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[mt][nt][v]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const float m_new = fmaxf(m[nt], mx);
-        const float m_use = (m_new == -__builtin_inff()) ? 0.0f : m_new;
-        const float alpha = __builtin_amdgcn_exp2f(m[nt] - m_use);
-        m[nt] = m_new;
+            for (int v = 0; v < 16; ++v) x = fmaxf(x, s[mt][nt][v]);
+        x = fmaxf(x, __shfl_xor(x, 32));
+        mx[nt] = x * c;
+        need[nt] = mx[nt] > m[nt] + kLazyRescale;
+    }
+    if (__any(need[0] || need[1])) {
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+            const float alpha = need[nt] ? __builtin_amdgcn_exp2f(m[nt] - mx[nt]) : 1.0f;
+            m[nt] = need[nt] ? mx[nt] : m[nt];
+            l[nt] *= alpha;
+            lt[nt] *= alpha;
+#pragma unroll
+            for (int md = 0; md < D / 32; ++md)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) o[md][nt][v] *= alpha;
+        }
+    }
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+        const float neg_m = (m[nt] == -__builtin_inff()) ? 0.0f : -m[nt];
         float rs = 0.0f;
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
-                const float p = __builtin_amdgcn_exp2f(s[mt][nt][v] - m_use);
+                const float p = __builtin_amdgcn_exp2f(fmaf(s[mt][nt][v], c, neg_m));
                 s[mt][nt][v] = p;
                 rs += p;
             }
-        l[nt] = l[nt] * alpha + rs;
-        lt[nt] = lt[nt] * alpha + (tail ? rs : 0.0f);
-#pragma unroll
-        for (int md = 0; md < D / 32; ++md)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) o[md][nt][v] *= alpha;
+        l[nt] += rs;
+        if (tail) lt[nt] += rs;
     }
 }
 
@@ -110,21 +121,24 @@ void attention_kernel(AttnArgs a) {
     const int work = xcd_remap(blockIdx.x, gridDim.x);
     const int bh = work / a.q_blocks;
     const int qb = work - bh * a.q_blocks;
+    const float c = a.scale_log2;
+
+    // Token of row r of block j is block_base(j) + intra_offset(r): the lane
+    // offsets are fixed, the block base is one scalar computation per block.
+    const int q_off[2] = {a.qmap.intra_offset(col), a.qmap.intra_offset(32 + col)};
+    const int k_off[2] = {a.kmap.intra_offset(col), a.kmap.intra_offset(32 + col)};
+    const char* q_head = a.q.data + a.q.row(bh, 0) * (int64_t)sizeof(T) + half * 16;
+    const char* k_head = a.k.data + a.k.row(bh, 0) * (int64_t)sizeof(T) + half * 16;
 
     // ---- query block: qs[nt*KT+t][lane] = Q[qb*64+nt*32+col][t*16+half*8 .. +7]
+    {
+        const int base = a.qmap.block_base(qb);
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-        const int qrow = qb * kBlock + nt * 32 + col;
-        const bool valid = qrow < a.q_tokens;
-        const char* base = a.q.data + a.q.row(bh, a.qmap(valid ? qrow : 0)) * (int64_t)sizeof(T);
+        for (int nt = 0; nt < 2; ++nt) {
+            const int tok = min(base + q_off[nt], a.q_tokens - 1);  // rows past the end are never stored
+            const char* p = q_head + (int64_t)tok * a.q.st * (int64_t)sizeof(T);
 #pragma unroll
-        for (int t = 0; t < KT; ++t) {
-            vec8 x;
-            if (valid) x = load8<vec8>(base + (t * 16 + half * 8) * sizeof(T));
-            else
-#pragma unroll
-                for (int e = 0; e < 8; ++e) x[e] = T(0.0f);
-            qs[nt * KT + t][lane] = x;
+            for (int t = 0; t < KT; ++t) qs[nt * KT + t][lane] = load8<vec8>(p + t * 32);
         }
     }
 
@@ -158,26 +172,24 @@ void attention_kernel(AttnArgs a) {
         }
     };
 
+    // Keys past the end of the sequence read the last row (a valid address);
+    // their scores are masked below and their V^T columns are zero.
+    auto load_k = [&](vec8 (&kf)[2][KT], int j) {
+        const int base = a.kmap.block_base(j);
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+            const int tok = min(base + k_off[mt], a.kv_tokens - 1);
+            const char* p = k_head + (int64_t)tok * a.k.st * (int64_t)sizeof(T);
+#pragma unroll
+            for (int t = 0; t < KT; ++t) kf[mt][t] = load8<vec8>(p + t * 32);
+        }
+    };
+
     // ---- exact chunks
     const int n_exact = SPARSE ? a.exact : a.kv_blocks;
     const int32_t* my_idx = SPARSE ? a.idx + ((int64_t)bh * a.q_blocks + qb) * a.exact : nullptr;
-    const char* vt_base = a.vt + (int64_t)bh * a.kv_blocks * D * kBlock * sizeof(T);
-
-    auto load_k = [&](vec8 (&kf)[2][KT], int j) {
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt) {
-            const int key = j * kBlock + mt * 32 + col;
-            const bool valid = key < a.kv_tokens;
-            const char* base = a.k.data + a.k.row(bh, a.kmap(valid ? key : 0)) * (int64_t)sizeof(T);
-#pragma unroll
-            for (int t = 0; t < KT; ++t) {
-                if (valid) kf[mt][t] = load8<vec8>(base + (t * 16 + half * 8) * sizeof(T));
-                else
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) kf[mt][t][e] = T(0.0f);
-            }
-        }
-    };
+    const char* vt_base = a.vt + (int64_t)bh * a.kv_blocks * D * kBlock * sizeof(T) +
+                          ((int64_t)col * kBlock + half * 8) * sizeof(T);
 
     vec8 kf[2][KT];
     if (n_exact > 0) load_k(kf, SPARSE ? my_idx[0] : 0);
@@ -192,66 +204,66 @@ void attention_kernel(AttnArgs a) {
         for (int md = 0; md < MD; ++md)
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks)
-                vf[md][ks] = load8<vec8>(vb + ((md * 32 + col) * kBlock + ks * 16 + half * 8) * sizeof(T));
+                vf[md][ks] = load8<vec8>(vb + (md * 32 * kBlock + ks * 16) * sizeof(T));
 
         f32x16 s[2][2];
         scores(kf, s);
-        const bool bounded = (j + 1) * kBlock > a.kv_tokens;
+        if (n + 1 < n_exact) load_k(kf, SPARSE ? my_idx[n + 1] : n + 1);
+
+        if ((j + 1) * kBlock > a.kv_tokens) {  // wave-uniform: only a short last block
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-            for (int nt = 0; nt < 2; ++nt)
+            for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
                 for (int v = 0; v < 16; ++v) {
                     const int key = j * kBlock + mt * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
-                    const float x = s[mt][nt][v] * a.scale_log2;
-                    s[mt][nt][v] = (bounded && key >= a.kv_tokens) ? -__builtin_inff() : x;
+                    if (key >= a.kv_tokens) {
+                        s[mt][0][v] = -__builtin_inff();
+                        s[mt][1][v] = -__builtin_inff();
+                    }
                 }
-        softmax_update<T, D>(s, m, l, lt, o, false);
-        if (n + 1 < n_exact) load_k(kf, SPARSE ? my_idx[n + 1] : n + 1);
+        }
+        softmax_update<T, D>(s, m, l, lt, o, c, false);
         pv_update<T, D>(s, vf, o);
     }
 
     // ---- tail chunks over the block centroids
     if (TAIL) {
         const uint32_t* mask = a.selmask + ((int64_t)bh * a.q_blocks + qb) * a.mask_words;
-        const char* kbar = a.kbar + (int64_t)bh * a.npad * D * sizeof(T);
-        const char* vbt = a.vbar_t + (int64_t)bh * D * a.npad * sizeof(T);
-        for (int c = 0; c < a.npad / kBlock; ++c) {
+        const char* kbar = a.kbar + ((int64_t)bh * a.npad * D + half * 8) * sizeof(T);
+        const char* vbt = a.vbar_t + ((int64_t)bh * D * a.npad + (int64_t)col * a.npad + half * 8) * sizeof(T);
+        for (int cb = 0; cb < a.npad / kBlock; ++cb) {
             asm volatile("" ::: "memory");
             vec8 cf[2][KT];
 #pragma unroll
             for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
                 for (int t = 0; t < KT; ++t)
-                    cf[mt][t] = load8<vec8>(kbar + ((int64_t)(c * kBlock + mt * 32 + col) * D + t * 16 + half * 8) * sizeof(T));
+                    cf[mt][t] = load8<vec8>(kbar + ((int64_t)(cb * kBlock + mt * 32 + col) * D + t * 16) * sizeof(T));
             vec8 vf[MD][4];
 #pragma unroll
             for (int md = 0; md < MD; ++md)
 #pragma unroll
                 for (int ks = 0; ks < 4; ++ks)
-                    vf[md][ks] = load8<vec8>(vbt + ((int64_t)(md * 32 + col) * a.npad + c * kBlock + ks * 16 + half * 8) * sizeof(T));
+                    vf[md][ks] = load8<vec8>(vbt + ((int64_t)md * 32 * a.npad + cb * kBlock + ks * 16) * sizeof(T));
             f32x16 s[2][2];
             scores(cf, s);
-            // centroid jc = 64c + 32mt + bit lives in selection word 2c + mt (wave uniform)
+            // centroid jc = 64cb + 32mt + bit lives in selection word 2cb + mt (wave uniform)
             uint32_t words[2];
 #pragma unroll
-            for (int mt = 0; mt < 2; ++mt) words[mt] = (2 * c + mt < a.mask_words) ? mask[2 * c + mt] : 0u;
+            for (int mt = 0; mt < 2; ++mt) words[mt] = (2 * cb + mt < a.mask_words) ? mask[2 * cb + mt] : 0u;
 #pragma unroll
             for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
                 for (int v = 0; v < 16; ++v) {
                     const int bit = 8 * (v >> 2) + 4 * half + (v & 3);
-                    const int jc = c * kBlock + mt * 32 + bit;
+                    const int jc = cb * kBlock + mt * 32 + bit;
                     const bool dead = jc >= a.centroids || ((words[mt] >> bit) & 1u);
                     const float bias = (jc == a.centroids - 1) ? a.last_len_log2 : 6.0f;  // log2(64)
 #pragma unroll
-                    for (int nt = 0; nt < 2; ++nt) {
-                        const float x = s[mt][nt][v] * a.scale_log2 + bias;
-                        s[mt][nt][v] = dead ? -__builtin_inff() : x;
-                    }
+                    for (int nt = 0; nt < 2; ++nt)
+                        s[mt][nt][v] = dead ? -__builtin_inff() : fmaf(s[mt][nt][v], c, bias);
                 }
-            softmax_update<T, D>(s, m, l, lt, o, true);
+            softmax_update<T, D>(s, m, l, lt, o, 1.0f, true);
             pv_update<T, D>(s, vf, o);
         }
     }
@@ -267,14 +279,17 @@ void attention_kernel(AttnArgs a) {
         wa[nt] = ltf * inv[nt] * a.corr_scale;
     }
     const bool first_order = TAIL && a.ht != nullptr;
-    const char* ht = first_order ? a.ht + (int64_t)bh * D * D * sizeof(T) : nullptr;
+    const char* ht = first_order ? a.ht + ((int64_t)bh * D * D + (int64_t)col * D + half * 8) * sizeof(T) : nullptr;
     char* obase[2];
     bool ovalid[2];
+    {
+        const int base = a.qmap.block_base(qb);
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-        const int qrow = qb * kBlock + nt * 32 + col;
-        ovalid[nt] = qrow < a.q_tokens;
-        obase[nt] = a.o.data + a.o.row(bh, a.qmap(ovalid[nt] ? qrow : 0)) * (int64_t)sizeof(T);
+        for (int nt = 0; nt < 2; ++nt) {
+            const int tok = base + q_off[nt];
+            ovalid[nt] = tok < a.q_tokens;
+            obase[nt] = a.o.data + a.o.row(bh, ovalid[nt] ? tok : 0) * (int64_t)sizeof(T);
+        }
     }
     typedef T vec4 __attribute__((ext_vector_type(4)));
 #pragma unroll
@@ -288,7 +303,7 @@ void attention_kernel(AttnArgs a) {
         if (first_order) {
 #pragma unroll
             for (int t = 0; t < KT; ++t) {
-                const vec8 hf = load8<vec8>(ht + ((md * 32 + col) * D + t * 16 + half * 8) * sizeof(T));
+                const vec8 hf = load8<vec8>(ht + (md * 32 * D + t * 16) * sizeof(T));
                 corr[0] = mfma32(hf, qs[t][lane], corr[0]);
                 corr[1] = mfma32(hf, qs[KT + t][lane], corr[1]);
             }

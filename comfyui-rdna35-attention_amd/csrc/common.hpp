@@ -124,6 +124,19 @@ struct TokenMap {
         const int tc = tile - tr * tiles_per_row;
         return f * frame_tokens + ((tr << 3) + (intra >> 3)) * width + (tc << 3) + (intra & 7);
     }
+    // token(64j + r) == block_base(j) + intra_offset(r) for 0 <= r < 64
+    __device__ __forceinline__ int block_base(int j) const {
+        if (frame_tokens == 0) return j << 6;
+        const int blocks_per_frame = frame_tokens >> 6;
+        const int f = j / blocks_per_frame;
+        const int tile = j - f * blocks_per_frame;
+        const int tr = tile / tiles_per_row;
+        const int tc = tile - tr * tiles_per_row;
+        return f * frame_tokens + (tr << 3) * width + (tc << 3);
+    }
+    __device__ __forceinline__ int intra_offset(int r) const {
+        return frame_tokens == 0 ? r : (r >> 3) * width + (r & 7);
+    }
 };
 
 inline TokenMap make_token_map(const pisa_token_grid& g) {
