@@ -152,7 +152,8 @@ struct ForwardBuffers {
     void* vm;
     float* hnorm;
     float* hpart;
-    void* vt;
+    void* kp;
+    void* vp;
     void* kbar_pad;
     void* vbar_t_pad;
     void* ht;
@@ -172,7 +173,8 @@ static ForwardBuffers carve_forward(void* ws, int bh, int tokens, int head_dim, 
     f.vm = c.take<void>(nd * esize);
     f.hnorm = c.take<float>((int64_t)bh * p.blocks * 4);
     f.hpart = c.take<float>((int64_t)bh * p.chunks * head_dim * head_dim * 4);
-    f.vt = c.take<void>(nd * pisa::kBlock * esize);
+    f.kp = c.take<void>(nd * pisa::kBlock * esize);
+    f.vp = c.take<void>(nd * pisa::kBlock * esize);
     f.kbar_pad = c.take<void>((int64_t)bh * p.npad * head_dim * esize);
     f.vbar_t_pad = c.take<void>((int64_t)bh * p.npad * head_dim * esize);
     f.ht = c.take<void>((int64_t)bh * head_dim * head_dim * esize);
@@ -292,7 +294,8 @@ static int prepare_impl(int32_t dtype, int32_t heads, int32_t tokens, int32_t he
     sa.hnorm_out = w.hnorm;
     sa.hpart = w.hpart;
     sa.qc_route = w.qc_route;
-    sa.vt_blocks = w.vt;
+    sa.kp_blocks = w.kp;
+    sa.vp_blocks = w.vp;
     sa.kbar_pad = w.kbar_pad;
     sa.vbar_t_pad = w.vbar_t_pad;
     sa.npad = p.npad;
@@ -341,11 +344,10 @@ static int attend_impl(int32_t dtype, int32_t heads, int32_t tokens, int32_t hea
     const pisa::TokenMap map = pisa::make_token_map(grid);
     pisa::AttnArgs aa;
     aa.q = to_view(q, heads);
-    aa.k = to_view(k, heads);
     aa.o = to_out(out, heads);
-    aa.vt = static_cast<const char*>(w.vt);
+    aa.kp = static_cast<const char*>(w.kp);
+    aa.vp = static_cast<const char*>(w.vp);
     aa.qmap = map;
-    aa.kmap = map;
     aa.q_tokens = tokens;
     aa.kv_tokens = tokens;
     aa.q_blocks = p.blocks;
@@ -576,7 +578,7 @@ int pisa_hip_fuse_spatial_epilogue(int32_t dtype, int32_t batch, int32_t heads, 
 int64_t attn_hip_dense_workspace_bytes(int32_t batch, int32_t heads, int32_t kv_tokens, int32_t head_dim) {
     if (batch <= 0 || heads <= 0 || kv_tokens <= 0 || head_dim <= 0) return 0;
     const int64_t blocks = (kv_tokens + pisa::kBlock - 1) / pisa::kBlock;
-    return (int64_t)batch * heads * blocks * head_dim * pisa::kBlock * 2;
+    return 2 * (int64_t)batch * heads * blocks * head_dim * pisa::kBlock * 2;  // packed K and V blocks
 }
 
 int attn_hip_dense_forward(int32_t dtype, int32_t batch, int32_t heads, int32_t q_tokens, int32_t kv_tokens,
@@ -602,17 +604,19 @@ int attn_hip_dense_forward(int32_t dtype, int32_t batch, int32_t heads, int32_t 
     hipStream_t st = static_cast<hipStream_t>(stream);
     const int bh = batch * heads;
     const int kv_blocks = (kv_tokens + pisa::kBlock - 1) / pisa::kBlock;
-    if ((rc = pisa::launch_vt_pack(dtype, head_dim, to_view(v, heads), kv_tokens, kv_blocks, bh,
-                                   static_cast<char*>(workspace), st)))
+    const int64_t table_bytes = need / 2;
+    char* kp = static_cast<char*>(workspace);
+    char* vp = kp + table_bytes;
+    if ((rc = pisa::launch_kv_pack(dtype, head_dim, to_view(k, heads), to_view(v, heads), kv_tokens, kv_blocks, bh,
+                                   kp, vp, st)))
         return rc;
     pisa::AttnArgs aa;
     memset(&aa, 0, sizeof(aa));
     aa.q = to_view(q, heads);
-    aa.k = to_view(k, heads);
     aa.o = to_out(out, heads);
-    aa.vt = static_cast<const char*>(workspace);
+    aa.kp = kp;
+    aa.vp = vp;
     aa.qmap = pisa::TokenMap{0, 0, 0};
-    aa.kmap = pisa::TokenMap{0, 0, 0};
     aa.q_tokens = q_tokens;
     aa.kv_tokens = kv_tokens;
     aa.q_blocks = (q_tokens + pisa::kBlock - 1) / pisa::kBlock;

@@ -1,16 +1,19 @@
-// Subsystems 3 and 4: exact attention on bf16/fp16 MFMA with the PISA tail,
-// first-order correction and merge fused into the epilogue.
+// Exact attention on bf16/fp16 MFMA with the PISA tail, first-order
+// correction and merge fused into the epilogue.
 //
 // One wavefront owns one 64-row query block (all four SIMDs of a CU run
 // independent query blocks, 1 wave per SIMD, up to 512 registers each).  The
-// wave keeps its query block in registers for the whole kernel and walks a
-// list of 64-key chunks:
+// wave keeps its query block in LDS for the whole kernel and walks one list of
+// 64-key chunks, with the operands of chunk c+1 in flight while chunk c is
+// computed:
 //   1. exact chunks: the key blocks the router selected (sparse) or every key
-//      block (dense), K rows read straight from the caller's layout and the
-//      transposed value block from the V^T table;
+//      block (dense);
 //   2. tail chunks (PISA only): the block centroids k_bar (dtype) as keys with
 //      score bias ln(len_j), -inf for selected blocks, v_bar as values;
-// accumulating one online softmax in fp32.  Scores are computed transposed,
+// accumulating one online softmax in fp32.  Every chunk is read from a packed
+// table (kfrag_elem / vfrag_elem order: one coalesced 1 KB load per MFMA
+// operand fragment) written by the statistics kernel or kv_pack_kernel.
+// Scores are computed transposed,
 //     S^T[key][query] = sum_d K[key][d] Q[query][d]          (32x32x16 MFMA)
 // so that a query is a lane column: row maxima need one lane exchange, and
 // the probabilities feed the second MFMA from their accumulator registers:
@@ -31,16 +34,38 @@ namespace pisa {
 
 constexpr float kLazyRescale = 8.0f;  // log2 headroom before the running max is moved
 
+// Sum of the 8 elements of a packed operand, fp32 accumulation (v_dot2 with ones).
+__device__ __forceinline__ float sum8(bf16x8 x, float acc) {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(x, x, 0, 1), one, acc, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(x, x, 2, 3), one, acc, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(x, x, 4, 5), one, acc, false);
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(x, x, 6, 7), one, acc, false);
+}
+__device__ __forceinline__ float sum8(f16x8 x, float acc) {
+    typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+    const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
+    acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(x, x, 0, 1), one, acc, false);
+    acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(x, x, 2, 3), one, acc, false);
+    acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(x, x, 4, 5), one, acc, false);
+    return __builtin_amdgcn_fdot2(__builtin_shufflevector(x, x, 6, 7), one, acc, false);
+}
+
 // Online-softmax update of one 64-key chunk held transposed in `s`
-// (s[mt][nt][v] = score of key 32mt + 8(v/4) + 4half + v%4, query 32nt + col).
-// `c` converts raw scores to the log2 domain (c = scale*log2(e) for exact
-// chunks, 1 for tail chunks whose scores are pre-converted).  The running max
-// only moves when a column's chunk max exceeds it by kLazyRescale, so the
-// O rescale (128 accumulators) runs on the first chunk and rarely after;
-// probabilities are then bounded by 2^kLazyRescale, well inside bf16/fp32.
+// (s[mt][nt][v] = score of key 32mt + 8(v/4) + 4half + v%4, query 32nt + col),
+// producing the probabilities as packed MFMA operands `pf[nt][ks]` (keys
+// 16ks .. 16ks+15).  `c` converts raw scores to the log2 domain
+// (c = scale*log2(e) for exact chunks, 1 for tail chunks whose scores are
+// pre-converted).  The running max only moves when a column's chunk max
+// exceeds it by kLazyRescale, so the O rescale (128 accumulators) runs on the
+// first chunk and rarely after; probabilities stay below 2^kLazyRescale.
+// The masses l (and lt for tail chunks) sum the rounded probabilities that
+// the PV product uses, so the weights of every output row sum to one.
 template <typename T, int D>
 __device__ __forceinline__ void softmax_update(f32x16 (&s)[2][2], float (&m)[2], float (&l)[2], float (&lt)[2],
-                                               f32x16 (&o)[D / 32][2], float c, bool tail) {
+                                               f32x16 (&o)[D / 32][2], float c, bool tail,
+                                               typename Elem<T>::vec8 (&pf)[2][4]) {
     float mx[2];
     bool need[2];
 #pragma unroll
@@ -74,10 +99,13 @@ __device__ __forceinline__ void softmax_update(f32x16 (&s)[2][2], float (&m)[2],
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const float p = __builtin_amdgcn_exp2f(fmaf(s[mt][nt][v], c, neg_m));
-                s[mt][nt][v] = p;
-                rs += p;
+            for (int ss = 0; ss < 2; ++ss) {
+                typename Elem<T>::vec8 p;
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    p[e] = from_f32<T>(__builtin_amdgcn_exp2f(fmaf(s[mt][nt][ss * 8 + e], c, neg_m)));
+                pf[nt][mt * 2 + ss] = p;
+                rs = sum8(p, rs);
             }
         l[nt] += rs;
         if (tail) lt[nt] += rs;
@@ -85,19 +113,9 @@ __device__ __forceinline__ void softmax_update(f32x16 (&s)[2][2], float (&m)[2],
 }
 
 template <typename T, int D>
-__device__ __forceinline__ void pv_update(const f32x16 (&p)[2][2],
+__device__ __forceinline__ void pv_update(const typename Elem<T>::vec8 (&pf)[2][4],
                                           const typename Elem<T>::vec8 (&vf)[D / 32][4],
                                           f32x16 (&o)[D / 32][2]) {
-    typedef typename Elem<T>::vec8 vec8;
-    vec8 pf[2][4];
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-            for (int ss = 0; ss < 2; ++ss)
-#pragma unroll
-                for (int j = 0; j < 8; ++j) pf[nt][mt * 2 + ss][j] = from_f32<T>(p[mt][nt][ss * 8 + j]);
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
@@ -108,10 +126,13 @@ __device__ __forceinline__ void pv_update(const f32x16 (&p)[2][2],
 
 template <typename T, int D, bool SPARSE, bool TAIL>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1)))
-void attention_kernel(AttnArgs a) {
+void attention_kernel(AttnArgs a, const int32_t* __restrict__ sel, const uint32_t* __restrict__ selmask) {
+    // sel/selmask are a.idx/a.selmask passed as restrict-qualified arguments: the
+    // kernel never writes them, so their wave-uniform reads become scalar loads.
     typedef typename Elem<T>::vec8 vec8;
     constexpr int KT = D / 16;
     constexpr int MD = D / 32;
+    constexpr int64_t kBlockBytes = (int64_t)D * kBlock * sizeof(T);
     // Query fragments live in LDS, lane-private (lane l owns bytes [16l, 16l+16)
     // of every 1 KB row), so reads are conflict free and need no barrier.
     __shared__ __attribute__((aligned(16))) vec8 qs[2 * KT][64];
@@ -123,15 +144,12 @@ void attention_kernel(AttnArgs a) {
     const int qb = work - bh * a.q_blocks;
     const float c = a.scale_log2;
 
-    // Token of row r of block j is block_base(j) + intra_offset(r): the lane
-    // offsets are fixed, the block base is one scalar computation per block.
+    // Token of row r of block j is block_base(j) + intra_offset(r).
     const int q_off[2] = {a.qmap.intra_offset(col), a.qmap.intra_offset(32 + col)};
-    const int k_off[2] = {a.kmap.intra_offset(col), a.kmap.intra_offset(32 + col)};
-    const char* q_head = a.q.data + a.q.row(bh, 0) * (int64_t)sizeof(T) + half * 16;
-    const char* k_head = a.k.data + a.k.row(bh, 0) * (int64_t)sizeof(T) + half * 16;
 
     // ---- query block: qs[nt*KT+t][lane] = Q[qb*64+nt*32+col][t*16+half*8 .. +7]
     {
+        const char* q_head = a.q.data + a.q.row(bh, 0) * (int64_t)sizeof(T) + half * 16;
         const int base = a.qmap.block_base(qb);
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) {
@@ -153,7 +171,53 @@ void attention_kernel(AttnArgs a) {
     float l[2] = {0.0f, 0.0f};
     float lt[2] = {0.0f, 0.0f};
 
-    auto scores = [&](const vec8 (&kf)[2][KT], f32x16 (&s)[2][2]) {
+    // ---- chunk list: [0, n_exact) exact blocks, [n_exact, n_chunks) centroid chunks
+    const int n_exact = SPARSE ? a.exact : a.kv_blocks;
+    const int n_chunks = n_exact + (TAIL ? a.npad / kBlock : 0);
+    const int32_t* my_idx = SPARSE ? sel + ((int64_t)bh * a.q_blocks + qb) * a.exact : nullptr;
+    const char* kp_head = a.kp + (int64_t)bh * a.kv_blocks * kBlockBytes + lane * 16;
+    const char* vp_head = a.vp + (int64_t)bh * a.kv_blocks * kBlockBytes + lane * 16;
+    const char* kc_head = TAIL ? a.kbar + (int64_t)bh * a.npad * D * sizeof(T) + lane * 16 : nullptr;
+    const char* vc_head = TAIL ? a.vbar_t + (int64_t)bh * a.npad * D * sizeof(T) + lane * 16 : nullptr;
+    // block id of exact chunk c (wave uniform, scalar load)
+    auto block_of = [&](int cc) { return SPARSE ? my_idx[cc] : cc; };
+    // byte offset of chunk cc in its table; chunks past the end re-read the
+    // last one, so every iteration issues the same loads
+    auto chunk_k = [&](int cc) -> const char* {
+        cc = min(cc, n_chunks - 1);
+        if (!TAIL || cc < n_exact) return kp_head + block_of(cc) * kBlockBytes;
+        return kc_head + (int64_t)(cc - n_exact) * kBlockBytes;
+    };
+    auto chunk_v = [&](int cc) -> const char* {
+        cc = min(cc, n_chunks - 1);
+        if (!TAIL || cc < n_exact) return vp_head + block_of(cc) * kBlockBytes;
+        return vc_head + (int64_t)(cc - n_exact) * kBlockBytes;
+    };
+    auto load_k = [&](vec8 (&kf)[2][KT], const char* p) {
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+            for (int t = 0; t < KT; ++t) kf[mt][t] = load8<vec8>(p + (mt * KT + t) * 1024);
+    };
+    auto load_v = [&](vec8 (&vf)[MD][4], const char* p) {
+#pragma unroll
+        for (int md = 0; md < MD; ++md)
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) vf[md][ks] = load8<vec8>(p + (md * 4 + ks) * 1024);
+    };
+
+    vec8 kf[2][KT];
+    vec8 vf[MD][4];
+    if (n_chunks > 0) {
+        load_k(kf, chunk_k(0));
+        load_v(vf, chunk_v(0));
+    }
+    for (int cc = 0; cc < n_chunks; ++cc) {
+        // Compiler barrier: keeps the query fragments in LDS instead of letting
+        // them be hoisted into (and exhaust) the register file.
+        asm volatile("" ::: "memory");
+        // ---- S^T = K Q^T
+        f32x16 s[2][2];
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
@@ -170,84 +234,28 @@ void attention_kernel(AttnArgs a) {
                 s[mt][1] = mfma32(kf[mt][t], q1, s[mt][1]);
             }
         }
-    };
+        load_k(kf, chunk_k(cc + 1));
 
-    // Keys past the end of the sequence read the last row (a valid address);
-    // their scores are masked below and their V^T columns are zero.
-    auto load_k = [&](vec8 (&kf)[2][KT], int j) {
-        const int base = a.kmap.block_base(j);
+        const bool tail = TAIL && cc >= n_exact;
+        if (!tail) {
+            const int j = block_of(cc);
+            if ((j + 1) * kBlock > a.kv_tokens) {  // wave-uniform: only a short last block
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt) {
-            const int tok = min(base + k_off[mt], a.kv_tokens - 1);
-            const char* p = k_head + (int64_t)tok * a.k.st * (int64_t)sizeof(T);
+                for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-            for (int t = 0; t < KT; ++t) kf[mt][t] = load8<vec8>(p + t * 32);
-        }
-    };
-
-    // ---- exact chunks
-    const int n_exact = SPARSE ? a.exact : a.kv_blocks;
-    const int32_t* my_idx = SPARSE ? a.idx + ((int64_t)bh * a.q_blocks + qb) * a.exact : nullptr;
-    const char* vt_base = a.vt + (int64_t)bh * a.kv_blocks * D * kBlock * sizeof(T) +
-                          ((int64_t)col * kBlock + half * 8) * sizeof(T);
-
-    vec8 kf[2][KT];
-    if (n_exact > 0) load_k(kf, SPARSE ? my_idx[0] : 0);
-    for (int n = 0; n < n_exact; ++n) {
-        // Compiler barrier: keeps the query fragments in LDS instead of letting
-        // them be hoisted into (and exhaust) the register file.
-        asm volatile("" ::: "memory");
-        const int j = SPARSE ? my_idx[n] : n;
-        vec8 vf[MD][4];
-        const char* vb = vt_base + (int64_t)j * D * kBlock * sizeof(T);
-#pragma unroll
-        for (int md = 0; md < MD; ++md)
-#pragma unroll
-            for (int ks = 0; ks < 4; ++ks)
-                vf[md][ks] = load8<vec8>(vb + (md * 32 * kBlock + ks * 16) * sizeof(T));
-
-        f32x16 s[2][2];
-        scores(kf, s);
-        if (n + 1 < n_exact) load_k(kf, SPARSE ? my_idx[n + 1] : n + 1);
-
-        if ((j + 1) * kBlock > a.kv_tokens) {  // wave-uniform: only a short last block
-#pragma unroll
-            for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    const int key = j * kBlock + mt * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
-                    if (key >= a.kv_tokens) {
-                        s[mt][0][v] = -__builtin_inff();
-                        s[mt][1][v] = -__builtin_inff();
+                    for (int v = 0; v < 16; ++v) {
+                        const int key = j * kBlock + mt * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
+                        if (key >= a.kv_tokens) {
+                            s[mt][0][v] = -__builtin_inff();
+                            s[mt][1][v] = -__builtin_inff();
+                        }
                     }
-                }
-        }
-        softmax_update<T, D>(s, m, l, lt, o, c, false);
-        pv_update<T, D>(s, vf, o);
-    }
-
-    // ---- tail chunks over the block centroids
-    if (TAIL) {
-        const uint32_t* mask = a.selmask + ((int64_t)bh * a.q_blocks + qb) * a.mask_words;
-        const char* kbar = a.kbar + ((int64_t)bh * a.npad * D + half * 8) * sizeof(T);
-        const char* vbt = a.vbar_t + ((int64_t)bh * D * a.npad + (int64_t)col * a.npad + half * 8) * sizeof(T);
-        for (int cb = 0; cb < a.npad / kBlock; ++cb) {
-            asm volatile("" ::: "memory");
-            vec8 cf[2][KT];
-#pragma unroll
-            for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-                for (int t = 0; t < KT; ++t)
-                    cf[mt][t] = load8<vec8>(kbar + ((int64_t)(cb * kBlock + mt * 32 + col) * D + t * 16) * sizeof(T));
-            vec8 vf[MD][4];
-#pragma unroll
-            for (int md = 0; md < MD; ++md)
-#pragma unroll
-                for (int ks = 0; ks < 4; ++ks)
-                    vf[md][ks] = load8<vec8>(vbt + ((int64_t)md * 32 * a.npad + cb * kBlock + ks * 16) * sizeof(T));
-            f32x16 s[2][2];
-            scores(cf, s);
-            // centroid jc = 64cb + 32mt + bit lives in selection word 2cb + mt (wave uniform)
+            }
+        } else {
+            // centroid jc = 64cb + 32mt + bit: selected blocks and padding -> -inf,
+            // others + log2(len_jc) (scores moved to the log2 domain here)
+            const int cb = cc - n_exact;
+            const uint32_t* mask = selmask + ((int64_t)bh * a.q_blocks + qb) * a.mask_words;
             uint32_t words[2];
 #pragma unroll
             for (int mt = 0; mt < 2; ++mt) words[mt] = (2 * cb + mt < a.mask_words) ? mask[2 * cb + mt] : 0u;
@@ -263,9 +271,11 @@ void attention_kernel(AttnArgs a) {
                     for (int nt = 0; nt < 2; ++nt)
                         s[mt][nt][v] = dead ? -__builtin_inff() : fmaf(s[mt][nt][v], c, bias);
                 }
-            softmax_update<T, D>(s, m, l, lt, o, 1.0f, true);
-            pv_update<T, D>(s, vf, o);
         }
+        vec8 pf[2][4];
+        softmax_update<T, D>(s, m, l, lt, o, tail ? 1.0f : c, tail, pf);
+        pv_update<T, D>(pf, vf, o);
+        load_v(vf, chunk_v(cc + 1));
     }
 
     // ---- epilogue: normalise, add the first-order correction one 32-dim
@@ -279,7 +289,8 @@ void attention_kernel(AttnArgs a) {
         wa[nt] = ltf * inv[nt] * a.corr_scale;
     }
     const bool first_order = TAIL && a.ht != nullptr;
-    const char* ht = first_order ? a.ht + ((int64_t)bh * D * D + (int64_t)col * D + half * 8) * sizeof(T) : nullptr;
+    // packed D x D matrix: fragment (md, t) = rows 32md.., columns 16t.. (kfrag_elem)
+    const char* ht = first_order ? a.ht + (int64_t)bh * D * D * sizeof(T) + lane * 16 : nullptr;
     char* obase[2];
     bool ovalid[2];
     {
@@ -303,7 +314,7 @@ void attention_kernel(AttnArgs a) {
         if (first_order) {
 #pragma unroll
             for (int t = 0; t < KT; ++t) {
-                const vec8 hf = load8<vec8>(ht + (md * 32 * D + t * 16) * sizeof(T));
+                const vec8 hf = load8<vec8>(ht + (md * KT + t) * 1024);
                 corr[0] = mfma32(hf, qs[t][lane], corr[0]);
                 corr[1] = mfma32(hf, qs[KT + t][lane], corr[1]);
             }
@@ -326,9 +337,13 @@ void attention_kernel(AttnArgs a) {
     }
 }
 
-// ---- transposed V blocks for dense attention: [BH][nblk][D][64], swap23 keys
+// ---- packed key and value blocks for dense attention (kfrag_elem /
+// vfrag_elem order; rows past kv_tokens are zero).  One workgroup per block:
+// 64 rows x D of K and V are read with 16-byte loads (4 rows per thread),
+// the key fragments are written straight from registers and the value block
+// is transposed through LDS.
 template <typename T, int D>
-__global__ __launch_bounds__(256) void vt_pack_kernel(View v, int kv_tokens, int kv_blocks, char* vt) {
+__global__ __launch_bounds__(256) void kv_pack_kernel(View k, View v, int kv_tokens, int kv_blocks, char* kp, char* vp) {
     typedef typename Elem<T>::vec8 vec8;
     typedef T vec4 __attribute__((ext_vector_type(4)));
     constexpr int kRow = kBlock + 8;
@@ -336,40 +351,52 @@ __global__ __launch_bounds__(256) void vt_pack_kernel(View v, int kv_tokens, int
     const int t = threadIdx.x;
     const int bh = blockIdx.x / kv_blocks;
     const int j = blockIdx.x - bh * kv_blocks;
-    constexpr int kChunks = D / 8;            // 16-byte pieces per row
-    constexpr int kRowsPerPass = 256 / kChunks;
-    const int c = t % kChunks;
-    const int r0 = t / kChunks;
+    constexpr int kPieces = D / 8;            // 16-byte pieces per row
+    constexpr int kRowsPerPass = 256 / kPieces;
+    const int pc = t % kPieces;
+    const int r0 = t / kPieces;
+    T* kdst = reinterpret_cast<T*>(kp) + ((int64_t)bh * kv_blocks + j) * D * kBlock;
+    T* vdst = reinterpret_cast<T*>(vp) + ((int64_t)bh * kv_blocks + j) * D * kBlock;
     for (int r = r0 * 4; r < kBlock; r += kRowsPerPass * 4) {
         vec8 x[4];
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
             const int key = j * kBlock + r + rr;
-            if (key < kv_tokens) x[rr] = load8<vec8>(v.data + (v.row(bh, key) + c * 8) * sizeof(T));
-            else
+            vec8 kx;
+            if (key < kv_tokens) {
+                kx = load8<vec8>(k.data + (k.row(bh, key) + pc * 8) * sizeof(T));
+                x[rr] = load8<vec8>(v.data + (v.row(bh, key) + pc * 8) * sizeof(T));
+            } else {
 #pragma unroll
-                for (int e = 0; e < 8; ++e) x[rr][e] = T(0.0f);
+                for (int e = 0; e < 8; ++e) {
+                    kx[e] = T(0.0f);
+                    x[rr][e] = T(0.0f);
+                }
+            }
+            store8(kdst + kfrag_elem(r + rr, pc * 8, D), kx);
         }
         const int p = swap23(r);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             vec4 w = {x[0][e], x[1][e], x[2][e], x[3][e]};
-            *reinterpret_cast<vec4*>(&lds[(c * 8 + e) * kRow + p]) = w;
+            *reinterpret_cast<vec4*>(&lds[(pc * 8 + e) * kRow + p]) = w;
         }
     }
     __syncthreads();
-    T* dst = reinterpret_cast<T*>(vt) + ((int64_t)bh * kv_blocks + j) * D * kBlock;
+    // value fragment f = 4md + ks, lane (half, col): row 32md + col, positions 16ks + 8half
     for (int id = t; id < D * 8; id += 256) {
-        const int d = id >> 3;
-        const int pc = id & 7;
-        store8(dst + d * kBlock + pc * 8, *reinterpret_cast<const vec8*>(&lds[d * kRow + pc * 8]));
+        const int f = id >> 6;
+        const int L = id & 63;
+        const int row = (f >> 2) * 32 + (L & 31);
+        const int pos = (f & 3) * 16 + (L >> 5) * 8;
+        store8(vdst + id * 8, *reinterpret_cast<const vec8*>(&lds[row * kRow + pos]));
     }
 }
 
 template <typename T, int D, bool SPARSE, bool TAIL>
 int launch_attention_t(const AttnArgs& a, int bh_count, hipStream_t stream) {
     const int waves = bh_count * a.q_blocks;
-    hipLaunchKernelGGL((attention_kernel<T, D, SPARSE, TAIL>), dim3(waves), dim3(64), 0, stream, a);
+    hipLaunchKernelGGL((attention_kernel<T, D, SPARSE, TAIL>), dim3(waves), dim3(64), 0, stream, a, a.idx, a.selmask);
     return pisa_host::check_launch("attention_kernel");
 }
 
@@ -393,17 +420,17 @@ int launch_attention(int dtype, int head_dim, bool sparse, bool tail, const Attn
     return launch_attention_t<f16_t, 64, false, false>(a, bh_count, stream);
 }
 
-int launch_vt_pack(int dtype, int head_dim, const View& v, int kv_tokens, int kv_blocks, int bh_count,
-                   char* vt, hipStream_t stream) {
+int launch_kv_pack(int dtype, int head_dim, const View& k, const View& v, int kv_tokens, int kv_blocks, int bh_count,
+                   char* kp, char* vp, hipStream_t stream) {
     const dim3 grid(bh_count * kv_blocks);
     if (dtype == PISA_DTYPE_BF16) {
-        if (head_dim == 128) hipLaunchKernelGGL((vt_pack_kernel<bf16_t, 128>), grid, dim3(256), 0, stream, v, kv_tokens, kv_blocks, vt);
-        else hipLaunchKernelGGL((vt_pack_kernel<bf16_t, 64>), grid, dim3(256), 0, stream, v, kv_tokens, kv_blocks, vt);
+        if (head_dim == 128) hipLaunchKernelGGL((kv_pack_kernel<bf16_t, 128>), grid, dim3(256), 0, stream, k, v, kv_tokens, kv_blocks, kp, vp);
+        else hipLaunchKernelGGL((kv_pack_kernel<bf16_t, 64>), grid, dim3(256), 0, stream, k, v, kv_tokens, kv_blocks, kp, vp);
     } else {
-        if (head_dim == 128) hipLaunchKernelGGL((vt_pack_kernel<f16_t, 128>), grid, dim3(256), 0, stream, v, kv_tokens, kv_blocks, vt);
-        else hipLaunchKernelGGL((vt_pack_kernel<f16_t, 64>), grid, dim3(256), 0, stream, v, kv_tokens, kv_blocks, vt);
+        if (head_dim == 128) hipLaunchKernelGGL((kv_pack_kernel<f16_t, 128>), grid, dim3(256), 0, stream, k, v, kv_tokens, kv_blocks, kp, vp);
+        else hipLaunchKernelGGL((kv_pack_kernel<f16_t, 64>), grid, dim3(256), 0, stream, k, v, kv_tokens, kv_blocks, kp, vp);
     }
-    return pisa_host::check_launch("vt_pack_kernel");
+    return pisa_host::check_launch("kv_pack_kernel");
 }
 
 }  // namespace pisa

@@ -86,6 +86,26 @@ __host__ __device__ __forceinline__ int swap23(int k) {
     return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1);
 }
 
+// ---------------------------------------------------------------- packed blocks
+// A 64-key block (or a 64-centroid chunk, or a D x D matrix read as D/32
+// "key" tiles) is stored as MFMA operand fragments of 64 lanes x 16 bytes,
+// each fragment contiguous, so the attention kernel reads one fragment with a
+// single fully coalesced 1 KB load (a row-major block would touch 32 cache
+// lines per load instruction, 32 bytes of each).
+//   key fragment (mt, t), t < D/16:  lane (half, col) holds
+//       K[32mt + col][16t + 8half .. +7]                 -> kfrag_elem
+//   value fragment (md, ks), ks < 4: lane (half, col) holds the keys at
+//       positions 16ks + 8half .. +7 of the swap23 order of V[.][32md + col]
+//                                                        -> vfrag_elem
+// Both return the element offset inside the block (block size 64 * D).
+__host__ __device__ __forceinline__ int kfrag_elem(int key, int d, int D) {
+    return ((((key >> 5) * (D >> 4) + (d >> 4)) * 64 + ((d >> 3) & 1) * 32 + (key & 31)) << 3) + (d & 7);
+}
+__host__ __device__ __forceinline__ int vfrag_elem(int key, int d) {
+    const int p = (key & ~12) | ((key & 4) << 1) | ((key & 8) >> 1);  // swap23(key)
+    return ((((d >> 5) * 4 + (p >> 4)) * 64 + ((p >> 3) & 1) * 32 + (d & 31)) << 3) + (p & 7);
+}
+
 // ---------------------------------------------------------------- views
 struct View {
     const char* data;  // byte pointer

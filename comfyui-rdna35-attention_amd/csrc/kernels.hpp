@@ -22,9 +22,10 @@ struct StatsArgs {
     float* hpart;      // [BH][chunks][D][D] (HYD / GENERIC)
     // attention operands (nullable)
     float* qc_route;   // [BH][N][D] f32 means for routing
-    void* vt_blocks;   // [BH][N][D][64] transposed V blocks, swap23 key order
-    void* kbar_pad;    // [BH][npad][D] dtype k_bar
-    void* vbar_t_pad;  // [BH][D][npad] dtype v_bar, swap23 centroid order
+    void* kp_blocks;   // [BH][N] packed key blocks (kfrag_elem order)
+    void* vp_blocks;   // [BH][N] packed value blocks (vfrag_elem order)
+    void* kbar_pad;    // [BH][npad/64] packed key chunks of dtype k_bar
+    void* vbar_t_pad;  // [BH][npad/64] packed value chunks of dtype v_bar
     int npad;
 };
 
@@ -35,7 +36,7 @@ struct ReduceArgs {
     const float* hpart;
     int chunks;
     float* hsum;       // [BH][D][D] (nullable)
-    void* ht;          // [BH][D][D] dtype, ht[c][r] = dtype(H_sum[r][c]) (nullable)
+    void* ht;          // [BH] packed D x D, element (c, r) = dtype(H_sum[r][c]) (nullable)
     void* kbar_pad;    // nullable
     void* vbar_t_pad;  // nullable
     int blocks, npad;
@@ -54,23 +55,24 @@ struct RouteArgs {
 };
 
 struct AttnArgs {
-    View q, k;
+    View q;
     OutView o;
-    const char* vt;   // [BH][kv_blocks][D][64] dtype, swap23 key order
-    TokenMap qmap, kmap;
+    const char* kp;   // [BH][kv_blocks] packed key blocks (kfrag_elem order)
+    const char* vp;   // [BH][kv_blocks] packed value blocks (vfrag_elem order)
+    TokenMap qmap;
     int q_tokens, kv_tokens, q_blocks, kv_blocks;
     float scale_log2;  // softmax scale * log2(e)
     // sparse exact chunks
     const int32_t* idx;  // [BH][q_blocks][exact]
     int exact;
     // tail chunks
-    const char* kbar;        // [BH][npad][D] dtype
-    const char* vbar_t;      // [BH][D][npad] dtype, swap23 centroid order
+    const char* kbar;        // [BH][npad/64] packed key chunks (centroids as keys)
+    const char* vbar_t;      // [BH][npad/64] packed value chunks
     const uint32_t* selmask; // [BH][q_blocks][mask_words]
     int mask_words, npad, centroids;
     float last_len_log2;     // log2(length of the last block)
     // first-order correction
-    const char* ht;          // [BH][D][D] dtype, ht[c][r] = H_sum[r][c]
+    const char* ht;          // [BH] packed D x D (kfrag_elem), element (c, r) = H_sum[r][c]
     float corr_scale;        // s / T
 };
 
@@ -87,8 +89,8 @@ int launch_stats_reduce(int dtype, const ReduceArgs& a, int bh_count, hipStream_
 int launch_route(const RouteArgs& a, hipStream_t stream);
 int launch_attention(int dtype, int head_dim, bool sparse, bool tail, const AttnArgs& a, int bh_count,
                      hipStream_t stream);
-int launch_vt_pack(int dtype, int head_dim, const View& v, int kv_tokens, int kv_blocks, int bh_count, char* vt,
-                   hipStream_t stream);
+int launch_kv_pack(int dtype, int head_dim, const View& k, const View& v, int kv_tokens, int kv_blocks, int bh_count,
+                   char* kp, char* vp, hipStream_t stream);
 int launch_fixed_block(int dtype, int head_dim, const View& q, const View& k, const View& v, const OutView& o,
                        int tokens, int bh_count, float scale, int causal, hipStream_t stream);
 int launch_pack(int dtype, const LayoutArgs& a, int bh_count, hipStream_t stream);

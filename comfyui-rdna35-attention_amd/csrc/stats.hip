@@ -1,4 +1,4 @@
-// Subsystem 1: per-64-token-block statistics on gfx950.
+// Per-64-token-block statistics on gfx950.
 //
 // One 256-thread workgroup owns `chunk_blocks` consecutive key blocks of one
 // (batch, head).  For every block it
@@ -11,8 +11,9 @@
 //   * computes H_b = (K - k_bar)^T V with 32x32x16 MFMAs (hi and lo passes,
 //     fp32 accumulation), its Frobenius norm, and accumulates H_b into a
 //     per-workgroup partial of H_sum held in the MFMA accumulators,
-//   * writes the transposed V block (the operand layout of the attention
-//     kernel) and the padded centroid tables used by the tail.
+//   * writes the key and value block packed as attention-kernel operand
+//     fragments (kfrag_elem / vfrag_elem) and the packed centroid chunks
+//     used by the tail.
 // The partial H_sum of each workgroup is written once; stats_reduce_kernel
 // sums the partials in a fixed order, so H_sum is deterministic (the
 // reference accumulates it with float atomicAdd, pisa_kernels.cu:227).
@@ -144,10 +145,9 @@ __global__ __launch_bounds__(kStatsThreads) void stats_kernel(StatsArgs a) {
             if (a.vm_f32) static_cast<float*>(a.vm_out)[o] = mv;
             else static_cast<T*>(a.vm_out)[o] = from_f32<T>(mv);
             if (a.qc_route) a.qc_route[o] = mq;
-            if (a.kbar_pad)
-                static_cast<T*>(a.kbar_pad)[((int64_t)bh * a.npad + b) * D + d] = from_f32<T>(mk);
-            if (a.vbar_t_pad)
-                static_cast<T*>(a.vbar_t_pad)[((int64_t)bh * D + d) * a.npad + swap23(b)] = from_f32<T>(mv);
+            const int64_t chunk_base = ((int64_t)bh * a.npad + (b & ~63)) * D;  // packed 64-centroid chunk
+            if (a.kbar_pad) static_cast<T*>(a.kbar_pad)[chunk_base + kfrag_elem(b & 63, d, D)] = from_f32<T>(mk);
+            if (a.vbar_t_pad) static_cast<T*>(a.vbar_t_pad)[chunk_base + vfrag_elem(b & 63, d)] = from_f32<T>(mv);
         }
         if (!kCov) {
             __syncthreads();
@@ -211,16 +211,24 @@ __global__ __launch_bounds__(kStatsThreads) void stats_kernel(StatsArgs a) {
         ss = wave_sum(ss);
         if (lane == 0) norm_part[wave] = ss;
 
-        // ---- transposed V block for the attention kernel
-        if (a.vt_blocks) {
-            T* dst = static_cast<T*>(a.vt_blocks) + ((int64_t)bh * a.blocks + b) * D * kBlock;
+        // ---- packed key and value blocks for the attention kernel
+        if (a.kp_blocks) {
+            T* dst = static_cast<T*>(a.kp_blocks) + ((int64_t)bh * a.blocks + b) * D * kBlock;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) store8(dst + kfrag_elem(rq * 4 + r, c16 * 8, D), kv[r]);
+        }
+        if (a.vp_blocks) {
+            // value fragment f = 4md + ks, lane (half, col): V^T row 32md + col,
+            // swap23 positions 16ks + 8half .. +7 (lds_v is stored in that order)
+            T* dst = static_cast<T*>(a.vp_blocks) + ((int64_t)bh * a.blocks + b) * D * kBlock;
 #pragma unroll
             for (int it = 0; it < 4; ++it) {
                 const int id = it * kStatsThreads + t;
-                const int d = id >> 3;
-                const int pc = id & 7;
-                const vec8 x = *reinterpret_cast<const vec8*>(&lds_v[d * kLdsRow + pc * 8]);
-                store8(dst + d * kBlock + pc * 8, x);
+                const int f = id >> 6;
+                const int L = id & 63;
+                const int row = (f >> 2) * 32 + (L & 31);
+                const int pos = (f & 3) * 16 + (L >> 5) * 8;
+                store8(dst + id * 8, *reinterpret_cast<const vec8*>(&lds_v[row * kLdsRow + pos]));
             }
         }
         __syncthreads();
@@ -269,20 +277,21 @@ __global__ __launch_bounds__(256) void stats_reduce_kernel(ReduceArgs a) {
         for (int it = 0; it < 4; ++it) {
             const int lr = it * 8 + (t >> 5);  // output row = H column
             const int lc = t & 31;
-            ht[(tc * 32 + lr) * D + tr * 32 + lc] = from_f32<T>(tile[lc][lr]);
+            ht[kfrag_elem(tc * 32 + lr, tr * 32 + lc, D)] = from_f32<T>(tile[lc][lr]);
         }
     }
     if (blockIdx.x == 0) {
+        // zero the centroids past the last block: their scores are masked to
+        // -inf, and a zero value keeps 0 * value finite in the PV product
         const int pad = a.npad - a.blocks;
-        if (a.kbar_pad)
-            for (int i = t; i < pad * D; i += 256)
-                static_cast<T*>(a.kbar_pad)[((int64_t)bh * a.npad + a.blocks) * D + i] = T(0.0f);
-        if (a.vbar_t_pad)
-            for (int i = t; i < pad * D; i += 256) {
-                const int d = i / pad;
-                const int j = a.blocks + (i - d * pad);
-                static_cast<T*>(a.vbar_t_pad)[((int64_t)bh * D + d) * a.npad + swap23(j)] = T(0.0f);
-            }
+        const int64_t head_base = (int64_t)bh * a.npad * D;
+        for (int i = t; i < pad * D; i += 256) {
+            const int j = a.blocks + i / D;
+            const int d = i - (i / D) * D;
+            const int64_t base = head_base + (int64_t)(j & ~63) * D;
+            if (a.kbar_pad) static_cast<T*>(a.kbar_pad)[base + kfrag_elem(j & 63, d, D)] = T(0.0f);
+            if (a.vbar_t_pad) static_cast<T*>(a.vbar_t_pad)[base + vfrag_elem(j & 63, d)] = T(0.0f);
+        }
     }
 }
 
