@@ -3,9 +3,9 @@
 //
 // One wavefront owns one 64-row query block (all four SIMDs of a CU run
 // independent query blocks, 1 wave per SIMD, up to 512 registers each).  The
-// wave keeps its query block in LDS for the whole kernel and walks one list of
-// 64-key chunks, with the operands of chunk c+1 in flight while chunk c is
-// computed:
+// wave keeps its query block in registers for the whole kernel and walks one
+// list of 64-key chunks, with the operands of chunk c+1 in flight while chunk
+// c is computed:
 //   1. exact chunks: the key blocks the router selected (sparse) or every key
 //      block (dense);
 //   2. tail chunks (PISA only): the block centroids k_bar (dtype) as keys with
@@ -52,29 +52,28 @@ __device__ __forceinline__ float sum8(f16x8 x, float acc) {
     return __builtin_amdgcn_fdot2(__builtin_shufflevector(x, x, 6, 7), one, acc, false);
 }
 
-// Online-softmax update of one 64-key chunk held transposed in `s`
-// (s[mt][nt][v] = score of key 32mt + 8(v/4) + 4half + v%4, query 32nt + col),
-// producing the probabilities as packed MFMA operands `pf[nt][ks]` (keys
-// 16ks .. 16ks+15).  `c` converts raw scores to the log2 domain
-// (c = scale*log2(e) for exact chunks, 1 for tail chunks whose scores are
-// pre-converted).  The running max only moves when a column's chunk max
-// exceeds it by kLazyRescale, so the O rescale (128 accumulators) runs on the
-// first chunk and rarely after; probabilities stay below 2^kLazyRescale.
-// The masses l (and lt for tail chunks) sum the rounded probabilities that
-// the PV product uses, so the weights of every output row sum to one.
-template <typename T, int D>
-__device__ __forceinline__ void softmax_update(f32x16 (&s)[2][2], float (&m)[2], float (&l)[2], float (&lt)[2],
-                                               f32x16 (&o)[D / 32][2], float c, bool tail,
-                                               typename Elem<T>::vec8 (&pf)[2][4]) {
+// The chunk loop works on 32-key half chunks.  For half h the running max is
+// updated first (a short branchy step), then one straight-line region issues
+// the 16 score MFMAs of half h+1 interleaved with the exponentials of half h,
+// and the 16 PV MFMAs of half h interleaved with the operand loads of the
+// next chunk, so that VALU, memory and MFMA work of one wave overlap.
+
+// Running-max update for half-chunk scores s[nt] (s[nt][v] = raw score of key
+// 8(v/4) + 4half + v%4 of the half, query 32nt + col); `c` converts raw
+// scores to log2 units.  The running max only moves when a column's max
+// exceeds it by kLazyRescale, so the O rescale (128 accumulators) runs on
+// the first half chunk and rarely after; probabilities stay below
+// 2^kLazyRescale.
+template <int MD>
+__device__ __forceinline__ void rescale_half(const f32x16 (&s)[2], float c, float (&m)[2], float (&l)[2],
+                                             float (&lt)[2], f32x16 (&o)[MD][2]) {
     float mx[2];
     bool need[2];
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
-        float x = -__builtin_inff();
+        float x = s[nt][0];
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) x = fmaxf(x, s[mt][nt][v]);
+        for (int v = 1; v < 16; ++v) x = fmaxf(x, s[nt][v]);
         x = fmaxf(x, __shfl_xor(x, 32));
         mx[nt] = x * c;
         need[nt] = mx[nt] > m[nt] + kLazyRescale;
@@ -87,41 +86,35 @@ __device__ __forceinline__ void softmax_update(f32x16 (&s)[2][2], float (&m)[2],
             l[nt] *= alpha;
             lt[nt] *= alpha;
 #pragma unroll
-            for (int md = 0; md < D / 32; ++md)
+            for (int md = 0; md < MD; ++md)
 #pragma unroll
                 for (int v = 0; v < 16; ++v) o[md][nt][v] *= alpha;
         }
     }
+}
+
+// Probabilities of a half chunk as packed PV operands pf[nt][ss] (keys
+// 16ss .. 16ss+15 of the half in swap23 order, which is the accumulator row
+// order), and their masses: l (and lt for tail chunks) sum the rounded
+// probabilities the PV product uses, so every output row's weights sum to 1.
+template <typename T>
+__device__ __forceinline__ void probs_half(const f32x16 (&s)[2], float c, const float (&m)[2], float (&l)[2],
+                                           float (&lt)[2], bool tail, typename Elem<T>::vec8 (&pf)[2][2]) {
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
         const float neg_m = (m[nt] == -__builtin_inff()) ? 0.0f : -m[nt];
         float rs = 0.0f;
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
+        for (int ss = 0; ss < 2; ++ss) {
+            typename Elem<T>::vec8 p;
 #pragma unroll
-            for (int ss = 0; ss < 2; ++ss) {
-                typename Elem<T>::vec8 p;
-#pragma unroll
-                for (int e = 0; e < 8; ++e)
-                    p[e] = from_f32<T>(__builtin_amdgcn_exp2f(fmaf(s[mt][nt][ss * 8 + e], c, neg_m)));
-                pf[nt][mt * 2 + ss] = p;
-                rs = sum8(p, rs);
-            }
+            for (int e = 0; e < 8; ++e) p[e] = from_f32<T>(__builtin_amdgcn_exp2f(fmaf(s[nt][ss * 8 + e], c, neg_m)));
+            pf[nt][ss] = p;
+            rs = sum8(p, rs);
+        }
         l[nt] += rs;
-        if (tail) lt[nt] += rs;
+        lt[nt] += tail ? rs : 0.0f;
     }
-}
-
-template <typename T, int D>
-__device__ __forceinline__ void pv_update(const typename Elem<T>::vec8 (&pf)[2][4],
-                                          const typename Elem<T>::vec8 (&vf)[D / 32][4],
-                                          f32x16 (&o)[D / 32][2]) {
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-        for (int md = 0; md < D / 32; ++md)
-#pragma unroll
-            for (int nt = 0; nt < 2; ++nt) o[md][nt] = mfma32(vf[md][ks], pf[nt][ks], o[md][nt]);
 }
 
 template <typename T, int D, bool SPARSE, bool TAIL>
@@ -129,13 +122,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void attention_kernel(AttnArgs a, const int32_t* __restrict__ sel, const uint32_t* __restrict__ selmask) {
     // sel/selmask are a.idx/a.selmask passed as restrict-qualified arguments: the
     // kernel never writes them, so their wave-uniform reads become scalar loads.
+    static_assert(!TAIL || D == 128, "the tail / first-order path is built for head_dim 128");
     typedef typename Elem<T>::vec8 vec8;
     constexpr int KT = D / 16;
     constexpr int MD = D / 32;
     constexpr int64_t kBlockBytes = (int64_t)D * kBlock * sizeof(T);
-    // Query fragments live in LDS, lane-private (lane l owns bytes [16l, 16l+16)
-    // of every 1 KB row), so reads are conflict free and need no barrier.
-    __shared__ __attribute__((aligned(16))) vec8 qs[2 * KT][64];
     const int lane = threadIdx.x;
     const int half = lane >> 5;
     const int col = lane & 31;
@@ -147,7 +138,9 @@ void attention_kernel(AttnArgs a, const int32_t* __restrict__ sel, const uint32_
     // Token of row r of block j is block_base(j) + intra_offset(r).
     const int q_off[2] = {a.qmap.intra_offset(col), a.qmap.intra_offset(32 + col)};
 
-    // ---- query block: qs[nt*KT+t][lane] = Q[qb*64+nt*32+col][t*16+half*8 .. +7]
+    // ---- query block: qreg[nt][t] = Q[qb*64+nt*32+col][t*16+half*8 .. +7],
+    // kept in registers for the whole kernel
+    vec8 qreg[2][KT];
     {
         const char* q_head = a.q.data + a.q.row(bh, 0) * (int64_t)sizeof(T) + half * 16;
         const int base = a.qmap.block_base(qb);
@@ -156,9 +149,23 @@ void attention_kernel(AttnArgs a, const int32_t* __restrict__ sel, const uint32_
             const int tok = min(base + q_off[nt], a.q_tokens - 1);  // rows past the end are never stored
             const char* p = q_head + (int64_t)tok * a.q.st * (int64_t)sizeof(T);
 #pragma unroll
-            for (int t = 0; t < KT; ++t) qs[nt * KT + t][lane] = load8<vec8>(p + t * 32);
+            for (int t = 0; t < KT; ++t) qreg[nt][t] = load8<vec8>(p + t * 32);
         }
     }
+    // Pins the query fragments to AGPRs (an empty asm with an "a" operand):
+    // the architectural VGPRs hold O, S and P, and leaving the choice to the
+    // register allocator makes it copy fragments between the two files.
+    // MFMA reads its B operand from AGPRs directly.
+    auto pin_q = [&]() {
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+            for (int t = 0; t < KT; ++t) {
+                f32x4 x = __builtin_bit_cast(f32x4, qreg[nt][t]);
+                asm volatile("" : "+a"(x));
+                qreg[nt][t] = __builtin_bit_cast(vec8, x);
+            }
+    };
 
     f32x16 o[MD][2];
 #pragma unroll
@@ -175,107 +182,133 @@ void attention_kernel(AttnArgs a, const int32_t* __restrict__ sel, const uint32_
     const int n_exact = SPARSE ? a.exact : a.kv_blocks;
     const int n_chunks = n_exact + (TAIL ? a.npad / kBlock : 0);
     const int32_t* my_idx = SPARSE ? sel + ((int64_t)bh * a.q_blocks + qb) * a.exact : nullptr;
+    const uint32_t* my_mask = TAIL ? selmask + ((int64_t)bh * a.q_blocks + qb) * a.mask_words : nullptr;
     const char* kp_head = a.kp + (int64_t)bh * a.kv_blocks * kBlockBytes + lane * 16;
     const char* vp_head = a.vp + (int64_t)bh * a.kv_blocks * kBlockBytes + lane * 16;
     const char* kc_head = TAIL ? a.kbar + (int64_t)bh * a.npad * D * sizeof(T) + lane * 16 : nullptr;
     const char* vc_head = TAIL ? a.vbar_t + (int64_t)bh * a.npad * D * sizeof(T) + lane * 16 : nullptr;
-    // block id of exact chunk c (wave uniform, scalar load)
-    auto block_of = [&](int cc) { return SPARSE ? my_idx[cc] : cc; };
-    // byte offset of chunk cc in its table; chunks past the end re-read the
-    // last one, so every iteration issues the same loads
-    auto chunk_k = [&](int cc) -> const char* {
-        cc = min(cc, n_chunks - 1);
-        if (!TAIL || cc < n_exact) return kp_head + block_of(cc) * kBlockBytes;
-        return kc_head + (int64_t)(cc - n_exact) * kBlockBytes;
+    // The first-order correction needs the packed D x D matrix (32 fragments):
+    // the last iteration loads it into kf (fragments 0..15) and vf (16..31)
+    // in place of the next chunk.
+    const bool first_order = TAIL && a.ht != nullptr;
+    const char* ht = first_order ? a.ht + (int64_t)bh * D * D * sizeof(T) + lane * 16 : nullptr;
+    // Chunks past the end re-read the last one, so every iteration issues the
+    // same loads (their results are never used).
+    auto is_tail = [&](int x) { return TAIL && min(x, n_chunks - 1) >= n_exact; };
+    auto table_row = [&](int x) -> int {  // block id, or centroid chunk id for tail chunks
+        x = min(x, n_chunks - 1);
+        if (TAIL && x >= n_exact) return x - n_exact;
+        return SPARSE ? my_idx[x] : x;
     };
-    auto chunk_v = [&](int cc) -> const char* {
-        cc = min(cc, n_chunks - 1);
-        if (!TAIL || cc < n_exact) return vp_head + block_of(cc) * kBlockBytes;
-        return vc_head + (int64_t)(cc - n_exact) * kBlockBytes;
-    };
-    auto load_k = [&](vec8 (&kf)[2][KT], const char* p) {
+    auto kptr = [&](int x, int row) { return (is_tail(x) ? kc_head : kp_head) + row * kBlockBytes; };
+    auto vptr = [&](int x, int row) { return (is_tail(x) ? vc_head : vp_head) + row * kBlockBytes; };
+
+    vec8 kf[2][KT];   // kf[mt]: key fragments of the next half chunk that uses them
+    vec8 vf[MD][4];   // value fragments; [.][0..1] first half, [.][2..3] second half
+    auto load_k_half = [&](vec8 (&k)[KT], const char* p, int mt) {
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-            for (int t = 0; t < KT; ++t) kf[mt][t] = load8<vec8>(p + (mt * KT + t) * 1024);
+        for (int t = 0; t < KT; ++t) k[t] = load8<vec8>(p + (mt * KT + t) * 1024);
     };
-    auto load_v = [&](vec8 (&vf)[MD][4], const char* p) {
+    auto load_v_half = [&](const char* p, int mt) {
 #pragma unroll
         for (int md = 0; md < MD; ++md)
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks) vf[md][ks] = load8<vec8>(p + (md * 4 + ks) * 1024);
+            for (int ss = 0; ss < 2; ++ss) vf[md][2 * mt + ss] = load8<vec8>(p + (md * 4 + 2 * mt + ss) * 1024);
     };
-
-    vec8 kf[2][KT];
-    vec8 vf[MD][4];
-    if (n_chunks > 0) {
-        load_k(kf, chunk_k(0));
-        load_v(vf, chunk_v(0));
-    }
-    for (int cc = 0; cc < n_chunks; ++cc) {
-        // Compiler barrier: keeps the query fragments in LDS instead of letting
-        // them be hoisted into (and exhaust) the register file.
-        asm volatile("" ::: "memory");
-        // ---- S^T = K Q^T
-        f32x16 s[2][2];
+    auto scores_half = [&](const vec8 (&k)[KT], f32x16 (&s)[2]) {
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
+        for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
-            for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-                for (int v = 0; v < 16; ++v) s[mt][nt][v] = 0.0f;
+            for (int v = 0; v < 16; ++v) s[nt][v] = 0.0f;
 #pragma unroll
         for (int t = 0; t < KT; ++t) {
-            const vec8 q0 = qs[t][lane];
-            const vec8 q1 = qs[KT + t][lane];
-#pragma unroll
-            for (int mt = 0; mt < 2; ++mt) {
-                s[mt][0] = mfma32(kf[mt][t], q0, s[mt][0]);
-                s[mt][1] = mfma32(kf[mt][t], q1, s[mt][1]);
-            }
+            s[0] = mfma32(k[t], qreg[0][t], s[0]);
+            s[1] = mfma32(k[t], qreg[1][t], s[1]);
         }
-        load_k(kf, chunk_k(cc + 1));
-
-        const bool tail = TAIL && cc >= n_exact;
-        if (!tail) {
-            const int j = block_of(cc);
-            if ((j + 1) * kBlock > a.kv_tokens) {  // wave-uniform: only a short last block
+    };
+    auto pv_half = [&](int mt, const vec8 (&pf)[2][2]) {
 #pragma unroll
-                for (int mt = 0; mt < 2; ++mt)
+        for (int ss = 0; ss < 2; ++ss)
 #pragma unroll
-                    for (int v = 0; v < 16; ++v) {
-                        const int key = j * kBlock + mt * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
-                        if (key >= a.kv_tokens) {
-                            s[mt][0][v] = -__builtin_inff();
-                            s[mt][1][v] = -__builtin_inff();
-                        }
-                    }
-            }
-        } else {
-            // centroid jc = 64cb + 32mt + bit: selected blocks and padding -> -inf,
-            // others + log2(len_jc) (scores moved to the log2 domain here)
-            const int cb = cc - n_exact;
-            const uint32_t* mask = selmask + ((int64_t)bh * a.q_blocks + qb) * a.mask_words;
-            uint32_t words[2];
+            for (int md = 0; md < MD; ++md)
 #pragma unroll
-            for (int mt = 0; mt < 2; ++mt) words[mt] = (2 * cb + mt < a.mask_words) ? mask[2 * cb + mt] : 0u;
-#pragma unroll
-            for (int mt = 0; mt < 2; ++mt)
+                for (int nt = 0; nt < 2; ++nt) o[md][nt] = mfma32(vf[md][2 * mt + ss], pf[nt][ss], o[md][nt]);
+    };
+    // Masks / tail bias of half mt of chunk x (row = its table row); returns
+    // the factor that converts the resulting scores to log2 units.
+    auto transform_half = [&](int x, int row, int mt, f32x16 (&s)[2]) -> float {
+        if (!is_tail(x)) {
+            if ((row + 1) * kBlock > a.kv_tokens) {  // wave-uniform: only a short last block
 #pragma unroll
                 for (int v = 0; v < 16; ++v) {
-                    const int bit = 8 * (v >> 2) + 4 * half + (v & 3);
-                    const int jc = cb * kBlock + mt * 32 + bit;
-                    const bool dead = jc >= a.centroids || ((words[mt] >> bit) & 1u);
-                    const float bias = (jc == a.centroids - 1) ? a.last_len_log2 : 6.0f;  // log2(64)
-#pragma unroll
-                    for (int nt = 0; nt < 2; ++nt)
-                        s[mt][nt][v] = dead ? -__builtin_inff() : fmaf(s[mt][nt][v], c, bias);
+                    const int key = row * kBlock + mt * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
+                    if (key >= a.kv_tokens) {
+                        s[0][v] = -__builtin_inff();
+                        s[1][v] = -__builtin_inff();
+                    }
                 }
+            }
+            return c;
         }
-        vec8 pf[2][4];
-        softmax_update<T, D>(s, m, l, lt, o, tail ? 1.0f : c, tail, pf);
-        pv_update<T, D>(pf, vf, o);
-        load_v(vf, chunk_v(cc + 1));
+        // centroid jc = 64row + 32mt + bit: selected blocks and padding -> -inf,
+        // others + log2(len_jc) (scores moved to log2 units here)
+        const uint32_t word = (2 * row + mt < a.mask_words) ? my_mask[2 * row + mt] : 0u;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int bit = 8 * (v >> 2) + 4 * half + (v & 3);
+            const int jc = row * kBlock + mt * 32 + bit;
+            const bool dead = jc >= a.centroids || ((word >> bit) & 1u);
+            const float bias = (jc == a.centroids - 1) ? a.last_len_log2 : 6.0f;  // log2(64)
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) s[nt][v] = dead ? -__builtin_inff() : fmaf(s[nt][v], c, bias);
+        }
+        return 1.0f;
+    };
+
+    f32x16 sa[2], sb[2];  // scores of the first / second half of the current chunk
+    int row0 = 0, row1 = 0;
+    if (n_chunks > 0) {
+        row0 = table_row(0);
+        row1 = table_row(1);
+        const char* k0 = kptr(0, row0);
+        const char* v0 = vptr(0, row0);
+        load_k_half(kf[0], k0, 0);
+        load_k_half(kf[1], k0, 1);
+        load_v_half(v0, 0);
+        load_v_half(v0, 1);
+        pin_q();
+        scores_half(kf[0], sa);
+        load_k_half(kf[0], kptr(1, row1), 0);
+    }
+    for (int cc = 0; cc < n_chunks; ++cc) {
+        pin_q();
+        const int row2 = table_row(cc + 2);
+        const bool tail = is_tail(cc);
+        const bool last = cc + 1 == n_chunks;
+        const char* kn = (first_order && last) ? ht : kptr(cc + 1, row1);
+        const char* vn = (first_order && last) ? ht + 16 * 1024 : vptr(cc + 1, row1);
+        const char* kn2 = (first_order && last) ? ht : kptr(cc + 2, row2);
+        vec8 pf[2][2];
+
+        // ---- first half: scores in sa (issued one half earlier)
+        const float ca = transform_half(cc, row0, 0, sa);
+        rescale_half<MD>(sa, ca, m, l, lt, o);
+        scores_half(kf[1], sb);
+        probs_half<T>(sa, ca, m, l, lt, tail, pf);
+        load_k_half(kf[1], kn, 1);
+        pv_half(0, pf);
+        load_v_half(vn, 0);
+
+        // ---- second half: scores in sb; also scores the next chunk's first half
+        const float cb = transform_half(cc, row0, 1, sb);
+        rescale_half<MD>(sb, cb, m, l, lt, o);
+        scores_half(kf[0], sa);
+        probs_half<T>(sb, cb, m, l, lt, tail, pf);
+        load_k_half(kf[0], kn2, 0);
+        pv_half(1, pf);
+        load_v_half(vn, 1);
+        row0 = row1;
+        row1 = row2;
     }
 
     // ---- epilogue: normalise, add the first-order correction one 32-dim
@@ -288,9 +321,6 @@ void attention_kernel(AttnArgs a, const int32_t* __restrict__ sel, const uint32_
         inv[nt] = 1.0f / lf;
         wa[nt] = ltf * inv[nt] * a.corr_scale;
     }
-    const bool first_order = TAIL && a.ht != nullptr;
-    // packed D x D matrix: fragment (md, t) = rows 32md.., columns 16t.. (kfrag_elem)
-    const char* ht = first_order ? a.ht + (int64_t)bh * D * D * sizeof(T) + lane * 16 : nullptr;
     char* obase[2];
     bool ovalid[2];
     {
@@ -305,18 +335,19 @@ void attention_kernel(AttnArgs a, const int32_t* __restrict__ sel, const uint32_
     typedef T vec4 __attribute__((ext_vector_type(4)));
 #pragma unroll
     for (int md = 0; md < MD; ++md) {
-        asm volatile("" ::: "memory");
         f32x16 corr[2];
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
             for (int v = 0; v < 16; ++v) corr[nt][v] = 0.0f;
         if (first_order) {
+            // packed D x D matrix fragment (md, t): rows 32md.., columns 16t..
+            // (kfrag_elem), in kf (md < 2) and vf (md >= 2) since the last iteration
 #pragma unroll
             for (int t = 0; t < KT; ++t) {
-                const vec8 hf = load8<vec8>(ht + (md * KT + t) * 1024);
-                corr[0] = mfma32(hf, qs[t][lane], corr[0]);
-                corr[1] = mfma32(hf, qs[KT + t][lane], corr[1]);
+                const vec8 hf = md < 2 ? kf[md & 1][t] : vf[(md >= 2 ? md - 2 : 0) * 2 + t / 4][t % 4];
+                corr[0] = mfma32(hf, qreg[0][t], corr[0]);
+                corr[1] = mfma32(hf, qreg[1][t], corr[1]);
             }
         }
 #pragma unroll
