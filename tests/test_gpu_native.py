@@ -116,6 +116,39 @@ def test_route_topk_is_bit_exact_on_its_scores(native):
             assert (idx.cpu().numpy() == (sink % n)).any(axis=-1).all()
 
 
+@pytest.mark.parametrize("n,head_dim,k,round_bf16", [(37, 64, 5, True), (64, 128, 64, False), (65, 32, 1, True),
+                                                     (300, 100, 40, True), (700, 256, 350, False),
+                                                     (1024, 128, 144, True)])
+def test_route_topk_sizes_bit_exact(native, n, head_dim, k, round_bf16):
+    gen = torch.Generator().manual_seed(n + head_dim)
+    bh = 2
+    qc = torch.randn((bh, n, head_dim), generator=gen)
+    kc = torch.randn((bh, n, head_dim), generator=gen)
+    kc[:, n // 2] = kc[:, n // 3]  # exact ties
+    hn = torch.rand((bh, n), generator=gen) + 0.1 if round_bf16 else None
+    scores, idx = native.route_topk(qc.cuda(), kc.cuda(), None if hn is None else hn.cuda(), k,
+                                    1 / math.sqrt(head_dim), -1, round_bf16=round_bf16)
+    np.testing.assert_array_equal(idx.cpu().numpy(), opisa.topk_ascending(np32(scores), k))
+    expected = opisa.route_scores(qc.numpy(), kc.numpy(), 1 / math.sqrt(head_dim),
+                                  None if hn is None else hn.numpy(), -1, round_bf16)
+    assert_close(np32(scores), expected, 1e-5, 1e-5, "route scores")
+
+
+def test_route_topk_nonfinite_scores_and_empty_selection(native):
+    gen = torch.Generator().manual_seed(7)
+    bh, n = 1, 90
+    qc = torch.randn((bh, n, D), generator=gen)
+    kc = torch.randn((bh, n, D), generator=gen)
+    kc[0, 3] = float("nan")     # NaN scores rank above +inf
+    kc[0, 8] = float("inf")
+    kc[0, 9] = -float("inf")
+    scores, idx = native.route_topk(qc.cuda(), kc.cuda(), None, 12, 0.1, None, round_bf16=False)
+    np.testing.assert_array_equal(idx.cpu().numpy(), opisa.topk_ascending(np32(scores), 12))
+    assert (idx.cpu().numpy() == 3).any(axis=-1).all()  # the NaN column is in every row's selection
+    _, none = native.route_topk(qc.cuda(), kc.cuda(), None, 0, 0.1, None, round_bf16=False)
+    assert none.shape == (bh, n, 0)
+
+
 def test_route_topk_ties_go_to_lowest_index(native):
     bh, n = 1, 200
     qc = torch.zeros((bh, n, D))
