@@ -60,31 +60,47 @@ __global__ __launch_bounds__(kStatsThreads) void stats_kernel(StatsArgs a) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) hp[nt][v] = 0.0f;
 
-    for (int b = first; b < last; ++b) {
+    // 4 rows x 8 dims of q, k, v of block b; rows past the end of a short last
+    // block read a valid row and are zeroed (no branch around the loads).
+    auto load_block = [&](int b, vec8 (&qv)[4], vec8 (&kv)[4], vec8 (&vv)[4]) {
         const int start = b * kBlock;
         const int len = min(kBlock, a.tokens - start);
-        const float inv_len = 1.0f / static_cast<float>(len);
-
-        // ---- load 4 rows x 8 dims of q, k, v
-        vec8 qv[4], kv[4], vv[4];
+        const int64_t off = (c16 * 8) * (int64_t)sizeof(T);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int tok = rq * 4 + r;
-            if (tok < len) {
-                const int raster = a.map(start + tok);
-                const int64_t off = (c16 * 8) * (int64_t)sizeof(T);
-                qv[r] = load8<vec8>(a.q.data + a.q.row(bh, raster) * sizeof(T) + off);
-                kv[r] = load8<vec8>(a.k.data + a.k.row(bh, raster) * sizeof(T) + off);
-                vv[r] = load8<vec8>(a.v.data + a.v.row(bh, raster) * sizeof(T) + off);
-            } else {
+            const int raster = a.map(start + min(tok, len - 1));
+            qv[r] = load8<vec8>(a.q.data + a.q.row(bh, raster) * sizeof(T) + off);
+            kv[r] = load8<vec8>(a.k.data + a.k.row(bh, raster) * sizeof(T) + off);
+            vv[r] = load8<vec8>(a.v.data + a.v.row(bh, raster) * sizeof(T) + off);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            if (rq * 4 + r >= len)
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
                     qv[r][e] = T(0.0f);
                     kv[r][e] = T(0.0f);
                     vv[r][e] = T(0.0f);
                 }
-            }
+    };
+
+    // Block b+1 is loaded while block b is reduced (the prefetch past the
+    // last block re-reads it).
+    vec8 nq[4], nk[4], nv[4];
+    if (first < last) load_block(first, nq, nk, nv);
+    for (int b = first; b < last; ++b) {
+        const int start = b * kBlock;
+        const int len = min(kBlock, a.tokens - start);
+        const float inv_len = 1.0f / static_cast<float>(len);
+        vec8 qv[4], kv[4], vv[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            qv[r] = nq[r];
+            kv[r] = nk[r];
+            vv[r] = nv[r];
         }
+        load_block(min(b + 1, last - 1), nq, nk, nv);
 
         // ---- column sums over this thread's 4 rows, then over the block
         float sq[8], sk[8], sv[8];
