@@ -20,6 +20,14 @@ Also measured in the same process:
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
 Prints one JSON line.
+
+``--profile-run`` runs only what the counter profiles need (a plain device
+copy of COPY_BYTES, then one prepare and PROFILE_ATTENDS attend launches) and
+prints nothing; it is the command profiled under rocprofv3 for the committed
+summaries in profiles/.  ``roofline.traffic`` is taken from
+profiles/attention_c4_traffic.json (HBM bytes per attend launch from the
+FETCH_SIZE / WRITE_SIZE counters, each scaled by the copy kernel's reading of
+its known size) when that file exists.
 """
 from __future__ import annotations
 
@@ -44,6 +52,9 @@ PEAK_BF16_FLOPS = 2.5e15  # MI355X dense bf16 MFMA (no sparsity)
 PEAK_HBM_BYTES = 8.0e12
 BASELINE_MS = 25.121  # reference, gfx1151
 METRIC = "PISA call ms + MFMA util %, bf16 B=2 H=16 T=9216 D=128, 23/144 blocks"
+COPY_BYTES = 1 << 30          # profile run: elementwise copy of 1 GiB (reads and writes COPY_BYTES)
+PROFILE_ATTENDS = 10
+TRAFFIC_FILE = REPO / "profiles" / "attention_c4_traffic.json"
 
 
 def algorithmic_flops() -> dict:
@@ -114,6 +125,40 @@ def cpu_baseline(q, k, v, sample_heads: int) -> dict:
     }
 
 
+def profile_run() -> int:
+    """The workload of the committed counter profiles: one copy of known size, then the C4 stages."""
+    import torch
+
+    import mi355x_pisa
+    from mi355x_pisa.synthetic import anima_qkv
+
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    src = torch.empty(COPY_BYTES // 2, dtype=torch.bfloat16, device=device).fill_(1.0)
+    dst = torch.empty_like(src)
+    torch.neg(src, out=dst)  # one elementwise kernel: reads and writes COPY_BYTES
+    torch.cuda.synchronize()
+    del src, dst
+    q, k, v = anima_qkv(batch=BATCH, heads=HEADS, side=SIDE, head_dim=HEAD_DIM, seed=0, device=device)
+    out4 = torch.empty((BATCH, TOKENS, HEADS * HEAD_DIM), dtype=q.dtype, device=device)
+    out4 = out4.view(BATCH, TOKENS, HEADS, HEAD_DIM).permute(0, 2, 1, 3)
+    plan = mi355x_pisa.PisaPlan(q, k, v, out4, EXACT, 1.0 / math.sqrt(HEAD_DIM), token_grid=(1, SIDE, SIDE))
+    plan.prepare()
+    for _ in range(PROFILE_ATTENDS):
+        plan.attend()
+    torch.cuda.synchronize()
+    return 0
+
+
+def measured_traffic():
+    """HBM bytes per attend launch from the committed counter profile, or None."""
+    try:
+        data = json.loads(TRAFFIC_FILE.read_text())
+        return int(data["bytes_per_launch"])
+    except (OSError, ValueError, KeyError):
+        return None
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--gpus", type=int, default=1)
@@ -121,7 +166,10 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--cpu-sample-heads", type=int, default=2)
+    parser.add_argument("--profile-run", action="store_true")
     args = parser.parse_args()
+    if args.profile_run:
+        return profile_run()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the path shards by (batch, head) "
               f"with no communication, so N GPUs run N independent shares.", file=sys.stderr)
@@ -188,7 +236,7 @@ def main() -> int:
             "peak": PEAK_BF16_FLOPS / 1e12,
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_BF16_FLOPS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(),
         },
         "mfma_util_pct": round(100 * achieved / PEAK_BF16_FLOPS, 2),
         "exact_tile_tflops": round(flops["exact"] / (attend_ms * 1e-3) / 1e12, 2),
