@@ -74,7 +74,7 @@ __device__ __forceinline__ void rescale_half(const f32x16 (&s)[2], float c, floa
         float x = s[nt][0];
 #pragma unroll
         for (int v = 1; v < 16; ++v) x = fmaxf(x, s[nt][v]);
-        x = fmaxf(x, __shfl_xor(x, 32));
+        x = max_xor32(x);
         mx[nt] = x * c;
         need[nt] = mx[nt] > m[nt] + kLazyRescale;
     }
@@ -316,8 +316,8 @@ void attention_kernel(AttnArgs a, const int32_t* __restrict__ sel, const uint32_
     float inv[2], wa[2];
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
-        const float lf = l[nt] + __shfl_xor(l[nt], 32);
-        const float ltf = lt[nt] + __shfl_xor(lt[nt], 32);
+        const float lf = add_xor32(l[nt]);
+        const float ltf = add_xor32(lt[nt]);
         inv[nt] = 1.0f / lf;
         wa[nt] = ltf * inv[nt] * a.corr_scale;
     }

@@ -69,14 +69,33 @@ template <typename V> __device__ __forceinline__ void store8(void* p, V v) {
     *reinterpret_cast<u32x4*>(p) = __builtin_bit_cast(u32x4, v);
 }
 
+// Cross-lane exchanges without the LDS crossbar.  v_permlane32_swap swaps the
+// upper 32 lanes of one register with the lower 32 lanes of another, so
+// applied to two copies of x it yields {x[l], x[l ^ 32]} in every lane
+// (in some order); v_permlane16_swap does the same for 16-lane rows,
+// {x[l], x[l ^ 16]}.  Sums and maxima of the pair are order independent.
+__device__ __forceinline__ float2 pair_xor32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float2 pair_xor16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float add_xor32(float x) { const float2 p = pair_xor32(x); return p.x + p.y; }
+__device__ __forceinline__ float add_xor16(float x) { const float2 p = pair_xor16(x); return p.x + p.y; }
+__device__ __forceinline__ float max_xor32(float x) { const float2 p = pair_xor32(x); return fmaxf(p.x, p.y); }
+
 __device__ __forceinline__ float wave_max(float x) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
     return x;
 }
 __device__ __forceinline__ float wave_sum(float x) {
+    x = add_xor32(x);
+    x = add_xor16(x);
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
+    for (int o = 8; o > 0; o >>= 1) x += __shfl_xor(x, o);
     return x;
 }
 

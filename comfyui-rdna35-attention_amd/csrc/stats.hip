@@ -29,6 +29,14 @@ namespace pisa {
 constexpr int kStatsThreads = 256;
 constexpr int kLdsRow = kBlock + 8;  // padded LDS row (elements) of a transposed block
 
+// Element (row d, token position p) of a transposed block in LDS.  The 16-byte
+// chunks of a row are XOR-swizzled by (d / 8) % 8: the staging writes (rows 8
+// apart across lanes) and the operand reads (32 consecutive rows) then hit at
+// most 2 lanes per bank, against 8 for the plain padded layout.
+__device__ __forceinline__ int stage_off(int d, int p) {
+    return d * kLdsRow + ((((p >> 3) ^ (d >> 3)) & 7) << 3) + (p & 7);
+}
+
 
 template <typename T, int MODE>
 __global__ __launch_bounds__(kStatsThreads) void stats_kernel(StatsArgs a) {
@@ -119,12 +127,9 @@ __global__ __launch_bounds__(kStatsThreads) void stats_kernel(StatsArgs a) {
                     xv += to_f32(vv[r][e]);
                 }
             }
-            xq += __shfl_xor(xq, 16);
-            xk += __shfl_xor(xk, 16);
-            xv += __shfl_xor(xv, 16);
-            xq += __shfl_xor(xq, 32);
-            xk += __shfl_xor(xk, 32);
-            xv += __shfl_xor(xv, 32);
+            xq = add_xor32(add_xor16(xq));
+            xk = add_xor32(add_xor16(xk));
+            xv = add_xor32(add_xor16(xv));
             sq[e] = xq;
             sk[e] = xk;
             sv[e] = xv;
@@ -190,9 +195,9 @@ __global__ __launch_bounds__(kStatsThreads) void stats_kernel(StatsArgs a) {
             vec4 h4 = {hi[0], hi[1], hi[2], hi[3]};
             vec4 l4 = {lo[0], lo[1], lo[2], lo[3]};
             vec4 v4 = {vt[0], vt[1], vt[2], vt[3]};
-            *reinterpret_cast<vec4*>(&lds_hi[d * kLdsRow + p0]) = h4;
-            if (MODE == PISA_STATS_HYD) *reinterpret_cast<vec4*>(&lds_lo[d * kLdsRow + p0]) = l4;
-            *reinterpret_cast<vec4*>(&lds_v[d * kLdsRow + p0]) = v4;
+            *reinterpret_cast<vec4*>(&lds_hi[stage_off(d, p0)]) = h4;
+            if (MODE == PISA_STATS_HYD) *reinterpret_cast<vec4*>(&lds_lo[stage_off(d, p0)]) = l4;
+            *reinterpret_cast<vec4*>(&lds_v[stage_off(d, p0)]) = v4;
         }
         __syncthreads();
 
@@ -205,13 +210,13 @@ __global__ __launch_bounds__(kStatsThreads) void stats_kernel(StatsArgs a) {
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
             const int pos = ks * 16 + half * 8;
-            const vec8 ah = *reinterpret_cast<const vec8*>(&lds_hi[(wave * 32 + col) * kLdsRow + pos]);
+            const vec8 ah = *reinterpret_cast<const vec8*>(&lds_hi[stage_off(wave * 32 + col, pos)]);
             vec8 al;
             if (MODE == PISA_STATS_HYD)
-                al = *reinterpret_cast<const vec8*>(&lds_lo[(wave * 32 + col) * kLdsRow + pos]);
+                al = *reinterpret_cast<const vec8*>(&lds_lo[stage_off(wave * 32 + col, pos)]);
 #pragma unroll
             for (int nt = 0; nt < 4; ++nt) {
-                const vec8 bv = *reinterpret_cast<const vec8*>(&lds_v[(nt * 32 + col) * kLdsRow + pos]);
+                const vec8 bv = *reinterpret_cast<const vec8*>(&lds_v[stage_off(nt * 32 + col, pos)]);
                 hb[nt] = mfma32(ah, bv, hb[nt]);
                 if (MODE == PISA_STATS_HYD) hb[nt] = mfma32(al, bv, hb[nt]);
             }
@@ -244,7 +249,7 @@ __global__ __launch_bounds__(kStatsThreads) void stats_kernel(StatsArgs a) {
                 const int L = id & 63;
                 const int row = (f >> 2) * 32 + (L & 31);
                 const int pos = (f & 3) * 16 + (L >> 5) * 8;
-                store8(dst + id * 8, *reinterpret_cast<const vec8*>(&lds_v[row * kLdsRow + pos]));
+                store8(dst + id * 8, *reinterpret_cast<const vec8*>(&lds_v[stage_off(row, pos)]));
             }
         }
         __syncthreads();
