@@ -53,7 +53,7 @@ PEAK_HBM_BYTES = 8.0e12
 BASELINE_MS = 25.121  # reference, gfx1151
 METRIC = "PISA call ms + MFMA util %, bf16 B=2 H=16 T=9216 D=128, 23/144 blocks"
 COPY_BYTES = 1 << 30          # profile run: elementwise copy of 1 GiB (reads and writes COPY_BYTES)
-PROFILE_ATTENDS = 10
+PROFILE_ATTENDS = 40
 TRAFFIC_FILE = REPO / "profiles" / "attention_c4_traffic.json"
 
 

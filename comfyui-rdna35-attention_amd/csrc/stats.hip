@@ -280,16 +280,32 @@ __global__ __launch_bounds__(256) void stats_reduce_kernel(ReduceArgs a) {
     const int tc = blockIdx.x & 3;   // 32-col tile index
     const int t = threadIdx.x;
     const float* src = a.hpart + (int64_t)bh * a.chunks * D * D;
+    // 4 elements per thread; the partials of 8 chunks are loaded together and
+    // added in chunk order (the sum does not depend on the load batching)
+    float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    int64_t off[4];
+#pragma unroll
+    for (int it = 0; it < 4; ++it) off[it] = (int64_t)(tr * 32 + it * 8 + (t >> 5)) * D + tc * 32 + (t & 31);
+    constexpr int kBatch = 8;
+    for (int ch0 = 0; ch0 < a.chunks; ch0 += kBatch) {
+        float x[kBatch][4];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u)
+#pragma unroll
+            for (int it = 0; it < 4; ++it)
+                x[u][it] = ch0 + u < a.chunks ? src[(int64_t)(ch0 + u) * D * D + off[it]] : 0.0f;
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u)
+#pragma unroll
+            for (int it = 0; it < 4; ++it)
+                if (ch0 + u < a.chunks) s[it] += x[u][it];
+    }
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
         const int lr = it * 8 + (t >> 5);
         const int lc = t & 31;
-        const int r = tr * 32 + lr;
-        const int c = tc * 32 + lc;
-        float s = 0.0f;
-        for (int ch = 0; ch < a.chunks; ++ch) s += src[(int64_t)ch * D * D + r * D + c];
-        if (a.hsum) a.hsum[(int64_t)bh * D * D + r * D + c] = s;
-        tile[lr][lc] = s;
+        if (a.hsum) a.hsum[(int64_t)bh * D * D + off[it]] = s[it];
+        tile[lr][lc] = s[it];
     }
     __syncthreads();
     if (a.ht) {
