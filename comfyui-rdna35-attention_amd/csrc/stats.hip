@@ -39,7 +39,7 @@ __device__ __forceinline__ int stage_off(int d, int p) {
 
 
 template <typename T, int MODE>
-__global__ __launch_bounds__(kStatsThreads) void stats_kernel(StatsArgs a) {
+__global__ __launch_bounds__(kStatsThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void stats_kernel(StatsArgs a) {
     constexpr int D = 128;
     typedef typename Elem<T>::vec8 vec8;
     __shared__ __attribute__((aligned(16))) T lds_hi[D * kLdsRow];
@@ -93,22 +93,22 @@ __global__ __launch_bounds__(kStatsThreads) void stats_kernel(StatsArgs a) {
                 }
     };
 
-    // Block b+1 is loaded while block b is reduced (the prefetch past the
-    // last block re-reads it).
-    vec8 nq[4], nk[4], nv[4];
-    if (first < last) load_block(first, nq, nk, nv);
+    // Two workgroups share each CU (at most 256 registers per lane), so one
+    // workgroup's loads overlap the other's reductions and MFMAs; a register
+    // prefetch of the next block would not fit that budget.
     for (int b = first; b < last; ++b) {
         const int start = b * kBlock;
         const int len = min(kBlock, a.tokens - start);
         const float inv_len = 1.0f / static_cast<float>(len);
         vec8 qv[4], kv[4], vv[4];
+        load_block(b, qv, kv, vv);
+        // ---- packed key block for the attention kernel (raw rows; rows past a
+        // short block are zero)
+        if (a.kp_blocks) {
+            T* dst = static_cast<T*>(a.kp_blocks) + ((int64_t)bh * a.blocks + b) * D * kBlock;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            qv[r] = nq[r];
-            kv[r] = nk[r];
-            vv[r] = nv[r];
+            for (int r = 0; r < 4; ++r) store8(dst + kfrag_elem(rq * 4 + r, c16 * 8, D), kv[r]);
         }
-        load_block(min(b + 1, last - 1), nq, nk, nv);
 
         // ---- column sums over this thread's 4 rows, then over the block
         float sq[8], sk[8], sv[8];
@@ -201,43 +201,38 @@ __global__ __launch_bounds__(kStatsThreads) void stats_kernel(StatsArgs a) {
         }
         __syncthreads();
 
-        // ---- H_b tile rows [32*wave, 32*wave+32) x all 128 columns
-        f32x16 hb[4];
-#pragma unroll
-        for (int nt = 0; nt < 4; ++nt)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) hb[nt][v] = 0.0f;
+        // ---- H_b tile rows [32*wave, 32*wave+32) x all 128 columns, one
+        // 32-column tile at a time (16 accumulators live; the row operands
+        // of the four 16-token steps are read once)
+        vec8 ah[4], al[4];
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
             const int pos = ks * 16 + half * 8;
-            const vec8 ah = *reinterpret_cast<const vec8*>(&lds_hi[stage_off(wave * 32 + col, pos)]);
-            vec8 al;
-            if (MODE == PISA_STATS_HYD)
-                al = *reinterpret_cast<const vec8*>(&lds_lo[stage_off(wave * 32 + col, pos)]);
-#pragma unroll
-            for (int nt = 0; nt < 4; ++nt) {
-                const vec8 bv = *reinterpret_cast<const vec8*>(&lds_v[stage_off(nt * 32 + col, pos)]);
-                hb[nt] = mfma32(ah, bv, hb[nt]);
-                if (MODE == PISA_STATS_HYD) hb[nt] = mfma32(al, bv, hb[nt]);
-            }
+            ah[ks] = *reinterpret_cast<const vec8*>(&lds_hi[stage_off(wave * 32 + col, pos)]);
+            if (MODE == PISA_STATS_HYD) al[ks] = *reinterpret_cast<const vec8*>(&lds_lo[stage_off(wave * 32 + col, pos)]);
         }
         float ss = 0.0f;
 #pragma unroll
-        for (int nt = 0; nt < 4; ++nt)
+        for (int nt = 0; nt < 4; ++nt) {
+            f32x16 hb;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) hb[v] = 0.0f;
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                const vec8 bv = *reinterpret_cast<const vec8*>(&lds_v[stage_off(nt * 32 + col, ks * 16 + half * 8)]);
+                hb = mfma32(ah[ks], bv, hb);
+                if (MODE == PISA_STATS_HYD) hb = mfma32(al[ks], bv, hb);
+            }
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
-                ss += hb[nt][v] * hb[nt][v];
-                hp[nt][v] += hb[nt][v];
+                ss += hb[v] * hb[v];
+                hp[nt][v] += hb[v];
             }
+        }
         ss = wave_sum(ss);
         if (lane == 0) norm_part[wave] = ss;
 
-        // ---- packed key and value blocks for the attention kernel
-        if (a.kp_blocks) {
-            T* dst = static_cast<T*>(a.kp_blocks) + ((int64_t)bh * a.blocks + b) * D * kBlock;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) store8(dst + kfrag_elem(rq * 4 + r, c16 * 8, D), kv[r]);
-        }
+        // ---- packed value block for the attention kernel
         if (a.vp_blocks) {
             // value fragment f = 4md + ks, lane (half, col): V^T row 32md + col,
             // swap23 positions 16ks + 8half .. +7 (lds_v is stored in that order)
