@@ -162,9 +162,16 @@ struct ForwardBuffers {
     int64_t total;
 };
 
+// Means and routing buffers have the real head dim; the packed tables the
+// attention kernel reads have the padded one.  H_sum partials and the packed
+// H_sum^T exist only at head dim 128 (the only width with the first-order
+// term and HYD statistics).
 static ForwardBuffers carve_forward(void* ws, int bh, int tokens, int head_dim, int exact, int esize) {
     const StatsPlan p = plan_stats(bh, tokens);
+    const int padded = pisa::padded_head_dim(head_dim) ? pisa::padded_head_dim(head_dim) : head_dim;
+    const int cov_dim = head_dim == 128 ? head_dim : 0;
     const int64_t nd = (int64_t)bh * p.blocks * head_dim;
+    const int64_t ndp = (int64_t)bh * p.blocks * padded;
     Carver c(ws);
     ForwardBuffers f;
     f.qc = c.take<void>(nd * esize);
@@ -172,12 +179,12 @@ static ForwardBuffers carve_forward(void* ws, int bh, int tokens, int head_dim, 
     f.kc = c.take<float>(nd * 4);
     f.vm = c.take<void>(nd * esize);
     f.hnorm = c.take<float>((int64_t)bh * p.blocks * 4);
-    f.hpart = c.take<float>((int64_t)bh * p.chunks * head_dim * head_dim * 4);
-    f.kp = c.take<void>(nd * pisa::kBlock * esize);
-    f.vp = c.take<void>(nd * pisa::kBlock * esize);
-    f.kbar_pad = c.take<void>((int64_t)bh * p.npad * head_dim * esize);
-    f.vbar_t_pad = c.take<void>((int64_t)bh * p.npad * head_dim * esize);
-    f.ht = c.take<void>((int64_t)bh * head_dim * head_dim * esize);
+    f.hpart = c.take<float>((int64_t)bh * p.chunks * cov_dim * cov_dim * 4);
+    f.kp = c.take<void>(ndp * pisa::kBlock * esize);
+    f.vp = c.take<void>(ndp * pisa::kBlock * esize);
+    f.kbar_pad = c.take<void>((int64_t)bh * p.npad * padded * esize);
+    f.vbar_t_pad = c.take<void>((int64_t)bh * p.npad * padded * esize);
+    f.ht = c.take<void>((int64_t)bh * cov_dim * cov_dim * esize);
     f.idx = c.take<int32_t>((int64_t)bh * p.blocks * (exact > 0 ? exact : 1) * 4);
     f.selmask = c.take<uint32_t>((int64_t)bh * p.blocks * p.mask_words * 4);
     f.total = c.off;
@@ -234,12 +241,21 @@ namespace pisa_host {
 static int validate_forward(int32_t dtype, int32_t batch, int32_t heads, int32_t tokens, int32_t head_dim,
                             const pisa_view& q, const pisa_view& k, const pisa_view& v, const pisa_view& out,
                             const pisa_token_grid& grid, int32_t exact_blocks, float scale, int32_t sink_block,
-                            int32_t stats_mode, int32_t route_mode, void* workspace, int64_t workspace_bytes,
-                            StatsPlan* plan) {
+                            int32_t stats_mode, int32_t route_mode, int32_t first_order, void* workspace,
+                            int64_t workspace_bytes, StatsPlan* plan) {
     if (!valid_dtype(dtype)) return fail(PISA_ERR_UNSUPPORTED, "PISA forward supports bf16 and fp16 only");
     if (batch <= 0 || heads <= 0 || tokens <= 0)
         return fail(PISA_ERR_INVALID_ARGUMENT, "PISA forward requires B>0, H>0, T>0");
-    if (head_dim != 128) return fail(PISA_ERR_UNSUPPORTED, "PISA forward requires head_dim=128, got %d", head_dim);
+    if (head_dim != 128) {
+        // generic_pisa.py:332-333: other head dims run without the first-order
+        // term, on centroid routing (no HYD bias, so no H_b norms)
+        if (!pisa::padded_head_dim(head_dim))
+            return fail(PISA_ERR_UNSUPPORTED, "PISA forward supports head_dim a multiple of 8 up to 256, got %d",
+                        head_dim);
+        if (stats_mode != PISA_STATS_GENERIC || route_mode != PISA_ROUTE_CENTROID || first_order)
+            return fail(PISA_ERR_UNSUPPORTED,
+                        "head_dim %d requires GENERIC statistics, CENTROID routing and no first-order term", head_dim);
+    }
     const int bh = batch * heads;
     const StatsPlan p = plan_stats(bh, tokens);
     if (p.blocks > pisa::kMaxRouteBlocks)
@@ -271,6 +287,10 @@ static int validate_forward(int32_t dtype, int32_t batch, int32_t heads, int32_t
     return PISA_OK;
 }
 
+static int route_impl(const ForwardBuffers& w, int32_t head_dim, int32_t exact_blocks, float scale,
+                      int32_t sink_block, int32_t route_mode, int32_t* debug_indices, float* debug_scores,
+                      const StatsPlan& p, int bh, hipStream_t st);
+
 static int prepare_impl(int32_t dtype, int32_t heads, int32_t tokens, int32_t head_dim, const pisa_view& q,
                         const pisa_view& k, const pisa_view& v, const pisa_token_grid& grid, int32_t exact_blocks,
                         float scale, int32_t sink_block, int32_t stats_mode, int32_t route_mode, int32_t first_order,
@@ -299,7 +319,17 @@ static int prepare_impl(int32_t dtype, int32_t heads, int32_t tokens, int32_t he
     sa.kbar_pad = w.kbar_pad;
     sa.vbar_t_pad = w.vbar_t_pad;
     sa.npad = p.npad;
+    sa.head_dim = head_dim;
     int rc;
+    if (head_dim != 128) {
+        const int padded = pisa::padded_head_dim(head_dim);
+        if ((rc = pisa::launch_stats_means(dtype, padded, sa, bh, st))) return rc;
+        if ((rc = pisa::launch_kv_pack(dtype, padded, head_dim, sa.k, sa.v, sa.map, tokens, p.blocks, bh,
+                                       static_cast<char*>(w.kp), static_cast<char*>(w.vp), st)))
+            return rc;
+        return route_impl(w, head_dim, exact_blocks, scale, sink_block, route_mode, debug_indices, debug_scores, p, bh,
+                          st);
+    }
     if ((rc = pisa::launch_stats(dtype, stats_mode, sa, bh, st))) return rc;
 
     pisa::ReduceArgs ra;
@@ -312,7 +342,13 @@ static int prepare_impl(int32_t dtype, int32_t heads, int32_t tokens, int32_t he
     ra.blocks = p.blocks;
     ra.npad = p.npad;
     if ((rc = pisa::launch_stats_reduce(dtype, ra, bh, st))) return rc;
+    return route_impl(w, head_dim, exact_blocks, scale, sink_block, route_mode, debug_indices, debug_scores, p, bh, st);
+}
 
+static int route_impl(const ForwardBuffers& w, int32_t head_dim, int32_t exact_blocks, float scale,
+                      int32_t sink_block, int32_t route_mode, int32_t* debug_indices, float* debug_scores,
+                      const StatsPlan& p, int bh, hipStream_t st) {
+    int rc;
     pisa::RouteArgs ro;
     ro.qc = w.qc_route;
     ro.kc = w.kc;
@@ -365,7 +401,8 @@ static int attend_impl(int32_t dtype, int32_t heads, int32_t tokens, int32_t hea
     aa.last_len_log2 = log2f(static_cast<float>(last_len));
     aa.ht = first_order ? static_cast<const char*>(w.ht) : nullptr;
     aa.corr_scale = scale / static_cast<float>(tokens);
-    return pisa::launch_attention(dtype, head_dim, true, true, aa, bh, st);
+    aa.head_dim = head_dim;
+    return pisa::launch_attention(dtype, pisa::padded_head_dim(head_dim), true, true, aa, bh, st);
 }
 
 }  // namespace pisa_host
@@ -379,7 +416,7 @@ int pisa_hip_forward(int32_t dtype, int32_t batch, int32_t heads, int32_t tokens
                      void* stream) {
     StatsPlan p;
     int rc = validate_forward(dtype, batch, heads, tokens, head_dim, q, k, v, out, grid, exact_blocks, scale,
-                              sink_block, stats_mode, route_mode, workspace, workspace_bytes, &p);
+                              sink_block, stats_mode, route_mode, first_order, workspace, workspace_bytes, &p);
     if (rc) return rc;
     hipStream_t st = static_cast<hipStream_t>(stream);
     const int bh = batch * heads;
@@ -396,7 +433,7 @@ int pisa_hip_prepare(int32_t dtype, int32_t batch, int32_t heads, int32_t tokens
                      void* workspace, int64_t workspace_bytes, void* stream) {
     StatsPlan p;
     int rc = validate_forward(dtype, batch, heads, tokens, head_dim, q, k, v, out, grid, exact_blocks, scale,
-                              sink_block, stats_mode, route_mode, workspace, workspace_bytes, &p);
+                              sink_block, stats_mode, route_mode, first_order, workspace, workspace_bytes, &p);
     if (rc) return rc;
     return prepare_impl(dtype, heads, tokens, head_dim, q, k, v, grid, exact_blocks, scale, sink_block, stats_mode,
                         route_mode, first_order, nullptr, nullptr, workspace, p, batch * heads,
@@ -409,7 +446,7 @@ int pisa_hip_attend(int32_t dtype, int32_t batch, int32_t heads, int32_t tokens,
                     void* workspace, int64_t workspace_bytes, void* stream) {
     StatsPlan p;
     int rc = validate_forward(dtype, batch, heads, tokens, head_dim, q, k, v, out, grid, exact_blocks, scale,
-                              sink_block, stats_mode, route_mode, workspace, workspace_bytes, &p);
+                              sink_block, stats_mode, route_mode, first_order, workspace, workspace_bytes, &p);
     if (rc) return rc;
     return attend_impl(dtype, heads, tokens, head_dim, q, k, out, grid, exact_blocks, scale, first_order, workspace, p,
                        batch * heads, static_cast<hipStream_t>(stream));
@@ -465,6 +502,7 @@ int pisa_hip_block_stats(int32_t dtype, int32_t out_dtype, int32_t batch, int32_
     sa.hnorm_out = cov ? h_norm : nullptr;
     sa.hpart = cov ? static_cast<float*>(workspace) : nullptr;
     sa.npad = p.npad;
+    sa.head_dim = head_dim;
     if ((rc = pisa::launch_stats(dtype, stats_mode, sa, bh, st))) return rc;
     if (!cov) return PISA_OK;
     pisa::ReduceArgs ra;
@@ -578,7 +616,8 @@ int pisa_hip_fuse_spatial_epilogue(int32_t dtype, int32_t batch, int32_t heads, 
 int64_t attn_hip_dense_workspace_bytes(int32_t batch, int32_t heads, int32_t kv_tokens, int32_t head_dim) {
     if (batch <= 0 || heads <= 0 || kv_tokens <= 0 || head_dim <= 0) return 0;
     const int64_t blocks = (kv_tokens + pisa::kBlock - 1) / pisa::kBlock;
-    return 2 * (int64_t)batch * heads * blocks * head_dim * pisa::kBlock * 2;  // packed K and V blocks
+    const int padded = pisa::padded_head_dim(head_dim) ? pisa::padded_head_dim(head_dim) : head_dim;
+    return 2 * (int64_t)batch * heads * blocks * padded * pisa::kBlock * 2;  // packed K and V blocks
 }
 
 int attn_hip_dense_forward(int32_t dtype, int32_t batch, int32_t heads, int32_t q_tokens, int32_t kv_tokens,
@@ -587,8 +626,10 @@ int attn_hip_dense_forward(int32_t dtype, int32_t batch, int32_t heads, int32_t 
     if (!valid_dtype(dtype)) return fail(PISA_ERR_UNSUPPORTED, "dense attention supports bf16 and fp16 only");
     if (batch <= 0 || heads <= 0 || q_tokens <= 0 || kv_tokens <= 0)
         return fail(PISA_ERR_INVALID_ARGUMENT, "requires B>0, H>0, Tq>0, Tk>0");
-    if (head_dim != 64 && head_dim != 128)
-        return fail(PISA_ERR_UNSUPPORTED, "dense attention supports head_dim 64 or 128, got %d", head_dim);
+    const int padded = pisa::padded_head_dim(head_dim);
+    if (!padded)
+        return fail(PISA_ERR_UNSUPPORTED, "dense attention supports head_dim a multiple of 8 up to 256, got %d",
+                    head_dim);
     if (!(scale > 0.0f) || scale == __builtin_inff()) return fail(PISA_ERR_INVALID_ARGUMENT, "scale must be positive and finite");
     int rc;
     if ((rc = check_view("q", q, 2, true)) || (rc = check_view("k", k, 2, true)) || (rc = check_view("v", v, 2, true)) ||
@@ -607,8 +648,8 @@ int attn_hip_dense_forward(int32_t dtype, int32_t batch, int32_t heads, int32_t 
     const int64_t table_bytes = need / 2;
     char* kp = static_cast<char*>(workspace);
     char* vp = kp + table_bytes;
-    if ((rc = pisa::launch_kv_pack(dtype, head_dim, to_view(k, heads), to_view(v, heads), kv_tokens, kv_blocks, bh,
-                                   kp, vp, st)))
+    if ((rc = pisa::launch_kv_pack(dtype, padded, head_dim, to_view(k, heads), to_view(v, heads),
+                                   pisa::TokenMap{0, 0, 0}, kv_tokens, kv_blocks, bh, kp, vp, st)))
         return rc;
     pisa::AttnArgs aa;
     memset(&aa, 0, sizeof(aa));
@@ -622,7 +663,8 @@ int attn_hip_dense_forward(int32_t dtype, int32_t batch, int32_t heads, int32_t 
     aa.q_blocks = (q_tokens + pisa::kBlock - 1) / pisa::kBlock;
     aa.kv_blocks = kv_blocks;
     aa.scale_log2 = scale * pisa::kLog2e;
-    return pisa::launch_attention(dtype, head_dim, false, false, aa, bh, st);
+    aa.head_dim = head_dim;
+    return pisa::launch_attention(dtype, padded, false, false, aa, bh, st);
 }
 
 int attn_hip_fixed_block_forward(int32_t dtype, int32_t batch, int32_t heads, int32_t tokens, int32_t head_dim,

@@ -2,10 +2,11 @@
 // correction and merge fused into the epilogue.
 //
 // One wavefront owns one 64-row query block (all four SIMDs of a CU run
-// independent query blocks, 1 wave per SIMD, up to 512 registers each).  The
-// wave keeps its query block in registers for the whole kernel and walks one
-// list of 64-key chunks, with the operands of chunk c+1 in flight while chunk
-// c is computed:
+// independent query blocks, 1 wave per SIMD, up to 512 registers each; at
+// padded head dims above 128 two waves split the block into 32-row halves).
+// The wave keeps its query rows in registers for the whole kernel and walks
+// one list of 64-key chunks, with the operands of chunk c+1 in flight while
+// chunk c is computed:
 //   1. exact chunks: the key blocks the router selected (sparse) or every key
 //      block (dense);
 //   2. tail chunks (PISA only): the block centroids k_bar (dtype) as keys with
@@ -59,28 +60,29 @@ __device__ __forceinline__ float sum8(f16x8 x, float acc) {
 // next chunk, so that VALU, memory and MFMA work of one wave overlap.
 
 // Running-max update for half-chunk scores s[nt] (s[nt][v] = raw score of key
-// 8(v/4) + 4half + v%4 of the half, query 32nt + col); `c` converts raw
-// scores to log2 units.  The running max only moves when a column's max
-// exceeds it by kLazyRescale, so the O rescale (128 accumulators) runs on
-// the first half chunk and rarely after; probabilities stay below
-// 2^kLazyRescale.
-template <int MD>
-__device__ __forceinline__ void rescale_half(const f32x16 (&s)[2], float c, float (&m)[2], float (&l)[2],
-                                             float (&lt)[2], f32x16 (&o)[MD][2]) {
-    float mx[2];
-    bool need[2];
+// 8(v/4) + 4half + v%4 of the half, query tile nt, column col); `c` converts
+// raw scores to log2 units.  The running max only moves when a column's max
+// exceeds it by kLazyRescale, so the O rescale runs on the first half chunk
+// and rarely after; probabilities stay below 2^kLazyRescale.
+template <int NT, int MD>
+__device__ __forceinline__ void rescale_half(const f32x16 (&s)[NT], float c, float (&m)[NT], float (&l)[NT],
+                                             float (&lt)[NT], f32x16 (&o)[MD][NT]) {
+    float mx[NT];
+    bool need[NT];
+    bool any_need = false;
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
+    for (int nt = 0; nt < NT; ++nt) {
         float x = s[nt][0];
 #pragma unroll
         for (int v = 1; v < 16; ++v) x = fmaxf(x, s[nt][v]);
         x = max_xor32(x);
         mx[nt] = x * c;
         need[nt] = mx[nt] > m[nt] + kLazyRescale;
+        any_need = any_need || need[nt];
     }
-    if (__any(need[0] || need[1])) {
+    if (__any(any_need)) {
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
+        for (int nt = 0; nt < NT; ++nt) {
             const float alpha = need[nt] ? __builtin_amdgcn_exp2f(m[nt] - mx[nt]) : 1.0f;
             m[nt] = need[nt] ? mx[nt] : m[nt];
             l[nt] *= alpha;
@@ -97,11 +99,11 @@ __device__ __forceinline__ void rescale_half(const f32x16 (&s)[2], float c, floa
 // 16ss .. 16ss+15 of the half in swap23 order, which is the accumulator row
 // order), and their masses: l (and lt for tail chunks) sum the rounded
 // probabilities the PV product uses, so every output row's weights sum to 1.
-template <typename T>
-__device__ __forceinline__ void probs_half(const f32x16 (&s)[2], float c, const float (&m)[2], float (&l)[2],
-                                           float (&lt)[2], bool tail, typename Elem<T>::vec8 (&pf)[2][2]) {
+template <typename T, int NT>
+__device__ __forceinline__ void probs_half(const f32x16 (&s)[NT], float c, const float (&m)[NT], float (&l)[NT],
+                                           float (&lt)[NT], bool tail, typename Elem<T>::vec8 (&pf)[NT][2]) {
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
+    for (int nt = 0; nt < NT; ++nt) {
         const float neg_m = (m[nt] == -__builtin_inff()) ? 0.0f : -m[nt];
         float rs = 0.0f;
 #pragma unroll
@@ -117,13 +119,19 @@ __device__ __forceinline__ void probs_half(const f32x16 (&s)[2], float c, const 
     }
 }
 
+// D is the padded head dim (padded_head_dim); a.head_dim <= D is the real
+// one.  A wave holds NT 32-row query tiles: both tiles of a 64-row block up to
+// D = 128, one tile (two waves per block) above, where the accumulators and
+// operands of 64 rows would not fit the 512 registers.
 template <typename T, int D, bool SPARSE, bool TAIL>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void attention_kernel(AttnArgs a, const int32_t* __restrict__ sel, const uint32_t* __restrict__ selmask) {
     // sel/selmask are a.idx/a.selmask passed as restrict-qualified arguments: the
     // kernel never writes them, so their wave-uniform reads become scalar loads.
-    static_assert(!TAIL || D == 128, "the tail / first-order path is built for head_dim 128");
+    static_assert(D % 32 == 0 && D <= 256, "padded head dim");
     typedef typename Elem<T>::vec8 vec8;
+    constexpr int NT = D <= 128 ? 2 : 1;  // 32-row query tiles per wave
+    constexpr int SUBS = 2 / NT;          // waves per 64-row query block
     constexpr int KT = D / 16;
     constexpr int MD = D / 32;
     constexpr int64_t kBlockBytes = (int64_t)D * kBlock * sizeof(T);
@@ -131,25 +139,37 @@ void attention_kernel(AttnArgs a, const int32_t* __restrict__ sel, const uint32_
     const int half = lane >> 5;
     const int col = lane & 31;
     const int work = xcd_remap(blockIdx.x, gridDim.x);
-    const int bh = work / a.q_blocks;
-    const int qb = work - bh * a.q_blocks;
+    const int block_work = work / SUBS;
+    const int sub = work - block_work * SUBS;
+    const int bh = block_work / a.q_blocks;
+    const int qb = block_work - bh * a.q_blocks;
     const float c = a.scale_log2;
 
-    // Token of row r of block j is block_base(j) + intra_offset(r).
-    const int q_off[2] = {a.qmap.intra_offset(col), a.qmap.intra_offset(32 + col)};
+    // Token of row r of block j is block_base(j) + intra_offset(r); this
+    // wave's rows are 32(sub + nt) + col.
+    int q_off[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) q_off[nt] = a.qmap.intra_offset(32 * (sub + nt) + col);
 
-    // ---- query block: qreg[nt][t] = Q[qb*64+nt*32+col][t*16+half*8 .. +7],
-    // kept in registers for the whole kernel
-    vec8 qreg[2][KT];
+    // ---- query rows: qreg[nt][t] = Q[row nt][t*16+half*8 .. +7] (zero past
+    // the real head dim), kept in registers for the whole kernel
+    vec8 qreg[NT][KT];
     {
         const char* q_head = a.q.data + a.q.row(bh, 0) * (int64_t)sizeof(T) + half * 16;
         const int base = a.qmap.block_base(qb);
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
+        for (int nt = 0; nt < NT; ++nt) {
             const int tok = min(base + q_off[nt], a.q_tokens - 1);  // rows past the end are never stored
             const char* p = q_head + (int64_t)tok * a.q.st * (int64_t)sizeof(T);
 #pragma unroll
-            for (int t = 0; t < KT; ++t) qreg[nt][t] = load8<vec8>(p + t * 32);
+            for (int t = 0; t < KT; ++t) {
+                if (D == 128 || t * 16 + half * 8 < a.head_dim) {
+                    qreg[nt][t] = load8<vec8>(p + t * 32);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) qreg[nt][t][e] = T(0.0f);
+                }
+            }
         }
     }
     // Pins the query fragments to AGPRs (an empty asm with an "a" operand):
@@ -158,7 +178,7 @@ void attention_kernel(AttnArgs a, const int32_t* __restrict__ sel, const uint32_
     // MFMA reads its B operand from AGPRs directly.
     auto pin_q = [&]() {
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
+        for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
             for (int t = 0; t < KT; ++t) {
                 f32x4 x = __builtin_bit_cast(f32x4, qreg[nt][t]);
@@ -167,16 +187,20 @@ void attention_kernel(AttnArgs a, const int32_t* __restrict__ sel, const uint32_
             }
     };
 
-    f32x16 o[MD][2];
+    f32x16 o[MD][NT];
 #pragma unroll
     for (int md = 0; md < MD; ++md)
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
+        for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
             for (int v = 0; v < 16; ++v) o[md][nt][v] = 0.0f;
-    float m[2] = {-__builtin_inff(), -__builtin_inff()};
-    float l[2] = {0.0f, 0.0f};
-    float lt[2] = {0.0f, 0.0f};
+    float m[NT], l[NT], lt[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        m[nt] = -__builtin_inff();
+        l[nt] = 0.0f;
+        lt[nt] = 0.0f;
+    }
 
     // ---- chunk list: [0, n_exact) exact blocks, [n_exact, n_chunks) centroid chunks
     const int n_exact = SPARSE ? a.exact : a.kv_blocks;
@@ -187,10 +211,10 @@ void attention_kernel(AttnArgs a, const int32_t* __restrict__ sel, const uint32_
     const char* vp_head = a.vp + (int64_t)bh * a.kv_blocks * kBlockBytes + lane * 16;
     const char* kc_head = TAIL ? a.kbar + (int64_t)bh * a.npad * D * sizeof(T) + lane * 16 : nullptr;
     const char* vc_head = TAIL ? a.vbar_t + (int64_t)bh * a.npad * D * sizeof(T) + lane * 16 : nullptr;
-    // The first-order correction needs the packed D x D matrix (32 fragments):
-    // the last iteration loads it into kf (fragments 0..15) and vf (16..31)
-    // in place of the next chunk.
-    const bool first_order = TAIL && a.ht != nullptr;
+    // The first-order correction (head dim 128 only) needs the packed D x D
+    // matrix (32 fragments): the last iteration loads it into kf (fragments
+    // 0..15) and vf (16..31) in place of the next chunk.
+    const bool first_order = TAIL && D == 128 && a.ht != nullptr;
     const char* ht = first_order ? a.ht + (int64_t)bh * D * D * sizeof(T) + lane * 16 : nullptr;
     // Chunks past the end re-read the last one, so every iteration issues the
     // same loads (their results are never used).
@@ -215,37 +239,35 @@ void attention_kernel(AttnArgs a, const int32_t* __restrict__ sel, const uint32_
 #pragma unroll
             for (int ss = 0; ss < 2; ++ss) vf[md][2 * mt + ss] = load8<vec8>(p + (md * 4 + 2 * mt + ss) * 1024);
     };
-    auto scores_half = [&](const vec8 (&k)[KT], f32x16 (&s)[2]) {
+    auto scores_half = [&](const vec8 (&k)[KT], f32x16 (&s)[NT]) {
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
+        for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
             for (int v = 0; v < 16; ++v) s[nt][v] = 0.0f;
 #pragma unroll
-        for (int t = 0; t < KT; ++t) {
-            s[0] = mfma32(k[t], qreg[0][t], s[0]);
-            s[1] = mfma32(k[t], qreg[1][t], s[1]);
-        }
+        for (int t = 0; t < KT; ++t)
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) s[nt] = mfma32(k[t], qreg[nt][t], s[nt]);
     };
-    auto pv_half = [&](int mt, const vec8 (&pf)[2][2]) {
+    auto pv_half = [&](int mt, const vec8 (&pf)[NT][2]) {
 #pragma unroll
         for (int ss = 0; ss < 2; ++ss)
 #pragma unroll
             for (int md = 0; md < MD; ++md)
 #pragma unroll
-                for (int nt = 0; nt < 2; ++nt) o[md][nt] = mfma32(vf[md][2 * mt + ss], pf[nt][ss], o[md][nt]);
+                for (int nt = 0; nt < NT; ++nt) o[md][nt] = mfma32(vf[md][2 * mt + ss], pf[nt][ss], o[md][nt]);
     };
     // Masks / tail bias of half mt of chunk x (row = its table row); returns
     // the factor that converts the resulting scores to log2 units.
-    auto transform_half = [&](int x, int row, int mt, f32x16 (&s)[2]) -> float {
+    auto transform_half = [&](int x, int row, int mt, f32x16 (&s)[NT]) -> float {
         if (!is_tail(x)) {
             if ((row + 1) * kBlock > a.kv_tokens) {  // wave-uniform: only a short last block
 #pragma unroll
                 for (int v = 0; v < 16; ++v) {
                     const int key = row * kBlock + mt * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
-                    if (key >= a.kv_tokens) {
-                        s[0][v] = -__builtin_inff();
-                        s[1][v] = -__builtin_inff();
-                    }
+                    if (key >= a.kv_tokens)
+#pragma unroll
+                        for (int nt = 0; nt < NT; ++nt) s[nt][v] = -__builtin_inff();
                 }
             }
             return c;
@@ -260,12 +282,12 @@ void attention_kernel(AttnArgs a, const int32_t* __restrict__ sel, const uint32_
             const bool dead = jc >= a.centroids || ((word >> bit) & 1u);
             const float bias = (jc == a.centroids - 1) ? a.last_len_log2 : 6.0f;  // log2(64)
 #pragma unroll
-            for (int nt = 0; nt < 2; ++nt) s[nt][v] = dead ? -__builtin_inff() : fmaf(s[nt][v], c, bias);
+            for (int nt = 0; nt < NT; ++nt) s[nt][v] = dead ? -__builtin_inff() : fmaf(s[nt][v], c, bias);
         }
         return 1.0f;
     };
 
-    f32x16 sa[2], sb[2];  // scores of the first / second half of the current chunk
+    f32x16 sa[NT], sb[NT];  // scores of the first / second half of the current chunk
     int row0 = 0, row1 = 0;
     if (n_chunks > 0) {
         row0 = table_row(0);
@@ -288,22 +310,22 @@ void attention_kernel(AttnArgs a, const int32_t* __restrict__ sel, const uint32_
         const char* kn = (first_order && last) ? ht : kptr(cc + 1, row1);
         const char* vn = (first_order && last) ? ht + 16 * 1024 : vptr(cc + 1, row1);
         const char* kn2 = (first_order && last) ? ht : kptr(cc + 2, row2);
-        vec8 pf[2][2];
+        vec8 pf[NT][2];
 
         // ---- first half: scores in sa (issued one half earlier)
         const float ca = transform_half(cc, row0, 0, sa);
-        rescale_half<MD>(sa, ca, m, l, lt, o);
+        rescale_half<NT, MD>(sa, ca, m, l, lt, o);
         scores_half(kf[1], sb);
-        probs_half<T>(sa, ca, m, l, lt, tail, pf);
+        probs_half<T, NT>(sa, ca, m, l, lt, tail, pf);
         load_k_half(kf[1], kn, 1);
         pv_half(0, pf);
         load_v_half(vn, 0);
 
         // ---- second half: scores in sb; also scores the next chunk's first half
         const float cb = transform_half(cc, row0, 1, sb);
-        rescale_half<MD>(sb, cb, m, l, lt, o);
+        rescale_half<NT, MD>(sb, cb, m, l, lt, o);
         scores_half(kf[0], sa);
-        probs_half<T>(sb, cb, m, l, lt, tail, pf);
+        probs_half<T, NT>(sb, cb, m, l, lt, tail, pf);
         load_k_half(kf[0], kn2, 0);
         pv_half(1, pf);
         load_v_half(vn, 1);
@@ -312,21 +334,22 @@ void attention_kernel(AttnArgs a, const int32_t* __restrict__ sel, const uint32_
     }
 
     // ---- epilogue: normalise, add the first-order correction one 32-dim
-    // tile at a time (keeps only 32 extra accumulators live), store
-    float inv[2], wa[2];
+    // tile at a time (keeps only 32 extra accumulators live), store the real
+    // head dims
+    float inv[NT], wa[NT];
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
+    for (int nt = 0; nt < NT; ++nt) {
         const float lf = add_xor32(l[nt]);
         const float ltf = add_xor32(lt[nt]);
         inv[nt] = 1.0f / lf;
         wa[nt] = ltf * inv[nt] * a.corr_scale;
     }
-    char* obase[2];
-    bool ovalid[2];
+    char* obase[NT];
+    bool ovalid[NT];
     {
         const int base = a.qmap.block_base(qb);
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
+        for (int nt = 0; nt < NT; ++nt) {
             const int tok = base + q_off[nt];
             ovalid[nt] = tok < a.q_tokens;
             obase[nt] = a.o.data + a.o.row(bh, ovalid[nt] ? tok : 0) * (int64_t)sizeof(T);
@@ -335,26 +358,30 @@ void attention_kernel(AttnArgs a, const int32_t* __restrict__ sel, const uint32_
     typedef T vec4 __attribute__((ext_vector_type(4)));
 #pragma unroll
     for (int md = 0; md < MD; ++md) {
-        f32x16 corr[2];
+        f32x16 corr[NT];
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
+        for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
             for (int v = 0; v < 16; ++v) corr[nt][v] = 0.0f;
-        if (first_order) {
-            // packed D x D matrix fragment (md, t): rows 32md.., columns 16t..
-            // (kfrag_elem), in kf (md < 2) and vf (md >= 2) since the last iteration
+        if constexpr (D == 128) {
+            if (first_order) {
+                // packed D x D matrix fragment (md, t): rows 32md.., columns 16t..
+                // (kfrag_elem), in kf (md < 2) and vf (md >= 2) since the last iteration
 #pragma unroll
-            for (int t = 0; t < KT; ++t) {
-                const vec8 hf = md < 2 ? kf[md & 1][t] : vf[(md >= 2 ? md - 2 : 0) * 2 + t / 4][t % 4];
-                corr[0] = mfma32(hf, qreg[0][t], corr[0]);
-                corr[1] = mfma32(hf, qreg[1][t], corr[1]);
+                for (int t = 0; t < KT; ++t) {
+                    const vec8 hf = md < 2 ? kf[md & 1][t] : vf[(md >= 2 ? md - 2 : 0) * 2 + t / 4][t % 4];
+#pragma unroll
+                    for (int nt = 0; nt < NT; ++nt) corr[nt] = mfma32(hf, qreg[nt][t], corr[nt]);
+                }
             }
         }
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
+        for (int nt = 0; nt < NT; ++nt) {
             if (!ovalid[nt]) continue;
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
+                const int d = md * 32 + 8 * g + 4 * half;
+                if (D != 128 && d >= a.head_dim) continue;
                 vec4 out;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
@@ -362,19 +389,21 @@ void attention_kernel(AttnArgs a, const int32_t* __restrict__ sel, const uint32_
                     if (first_order) x += corr[nt][4 * g + e] * wa[nt];
                     out[e] = from_f32<T>(x);
                 }
-                *reinterpret_cast<vec4*>(obase[nt] + (md * 32 + 8 * g + 4 * half) * sizeof(T)) = out;
+                *reinterpret_cast<vec4*>(obase[nt] + d * sizeof(T)) = out;
             }
         }
     }
 }
 
-// ---- packed key and value blocks for dense attention (kfrag_elem /
-// vfrag_elem order; rows past kv_tokens are zero).  One workgroup per block:
-// 64 rows x D of K and V are read with 16-byte loads (4 rows per thread),
-// the key fragments are written straight from registers and the value block
-// is transposed through LDS.
+// ---- packed key and value blocks (kfrag_elem / vfrag_elem order at the
+// padded width D; dims >= d_real and rows >= kv_tokens are zero; block j
+// row r is token map(64 j + r)).  One workgroup per block: 64 rows x D of K
+// and V are read with 16-byte loads (4 rows per thread), the key fragments are
+// written straight from registers and the value block is transposed through
+// LDS.
 template <typename T, int D>
-__global__ __launch_bounds__(256) void kv_pack_kernel(View k, View v, int kv_tokens, int kv_blocks, char* kp, char* vp) {
+__global__ __launch_bounds__(256) void kv_pack_kernel(View k, View v, TokenMap map, int kv_tokens, int kv_blocks,
+                                                      int d_real, char* kp, char* vp) {
     typedef typename Elem<T>::vec8 vec8;
     typedef T vec4 __attribute__((ext_vector_type(4)));
     constexpr int kRow = kBlock + 8;
@@ -386,6 +415,7 @@ __global__ __launch_bounds__(256) void kv_pack_kernel(View k, View v, int kv_tok
     constexpr int kRowsPerPass = 256 / kPieces;
     const int pc = t % kPieces;
     const int r0 = t / kPieces;
+    const bool live_d = pc * 8 < d_real;      // d_real is a multiple of 8
     T* kdst = reinterpret_cast<T*>(kp) + ((int64_t)bh * kv_blocks + j) * D * kBlock;
     T* vdst = reinterpret_cast<T*>(vp) + ((int64_t)bh * kv_blocks + j) * D * kBlock;
     for (int r = r0 * 4; r < kBlock; r += kRowsPerPass * 4) {
@@ -394,9 +424,10 @@ __global__ __launch_bounds__(256) void kv_pack_kernel(View k, View v, int kv_tok
         for (int rr = 0; rr < 4; ++rr) {
             const int key = j * kBlock + r + rr;
             vec8 kx;
-            if (key < kv_tokens) {
-                kx = load8<vec8>(k.data + (k.row(bh, key) + pc * 8) * sizeof(T));
-                x[rr] = load8<vec8>(v.data + (v.row(bh, key) + pc * 8) * sizeof(T));
+            if (key < kv_tokens && live_d) {
+                const int tok = map(key);
+                kx = load8<vec8>(k.data + (k.row(bh, tok) + pc * 8) * sizeof(T));
+                x[rr] = load8<vec8>(v.data + (v.row(bh, tok) + pc * 8) * sizeof(T));
             } else {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
@@ -426,42 +457,65 @@ __global__ __launch_bounds__(256) void kv_pack_kernel(View k, View v, int kv_tok
 
 template <typename T, int D, bool SPARSE, bool TAIL>
 int launch_attention_t(const AttnArgs& a, int bh_count, hipStream_t stream) {
-    const int waves = bh_count * a.q_blocks;
+    constexpr int kSubs = D <= 128 ? 1 : 2;  // waves per query block
+    const int waves = bh_count * a.q_blocks * kSubs;
     hipLaunchKernelGGL((attention_kernel<T, D, SPARSE, TAIL>), dim3(waves), dim3(64), 0, stream, a, a.idx, a.selmask);
     return pisa_host::check_launch("attention_kernel");
 }
 
-int launch_attention(int dtype, int head_dim, bool sparse, bool tail, const AttnArgs& a, int bh_count,
-                     hipStream_t stream) {
-    if (dtype == PISA_DTYPE_BF16) {
-        if (head_dim == 128) {
-            if (sparse) return tail ? launch_attention_t<bf16_t, 128, true, true>(a, bh_count, stream)
-                                    : launch_attention_t<bf16_t, 128, true, false>(a, bh_count, stream);
-            return tail ? launch_attention_t<bf16_t, 128, false, true>(a, bh_count, stream)
-                        : launch_attention_t<bf16_t, 128, false, false>(a, bh_count, stream);
-        }
-        return launch_attention_t<bf16_t, 64, false, false>(a, bh_count, stream);
-    }
-    if (head_dim == 128) {
-        if (sparse) return tail ? launch_attention_t<f16_t, 128, true, true>(a, bh_count, stream)
-                                : launch_attention_t<f16_t, 128, true, false>(a, bh_count, stream);
-        return tail ? launch_attention_t<f16_t, 128, false, true>(a, bh_count, stream)
-                    : launch_attention_t<f16_t, 128, false, false>(a, bh_count, stream);
-    }
-    return launch_attention_t<f16_t, 64, false, false>(a, bh_count, stream);
+template <typename T, int D>
+int launch_attention_d(bool sparse, bool tail, const AttnArgs& a, int bh_count, hipStream_t stream) {
+    if (sparse && tail) return launch_attention_t<T, D, true, true>(a, bh_count, stream);
+    if (!sparse && !tail) return launch_attention_t<T, D, false, false>(a, bh_count, stream);
+    return pisa_host::fail(PISA_ERR_UNSUPPORTED, "attention kernel: sparse and tail go together");
 }
 
-int launch_kv_pack(int dtype, int head_dim, const View& k, const View& v, int kv_tokens, int kv_blocks, int bh_count,
-                   char* kp, char* vp, hipStream_t stream) {
-    const dim3 grid(bh_count * kv_blocks);
-    if (dtype == PISA_DTYPE_BF16) {
-        if (head_dim == 128) hipLaunchKernelGGL((kv_pack_kernel<bf16_t, 128>), grid, dim3(256), 0, stream, k, v, kv_tokens, kv_blocks, kp, vp);
-        else hipLaunchKernelGGL((kv_pack_kernel<bf16_t, 64>), grid, dim3(256), 0, stream, k, v, kv_tokens, kv_blocks, kp, vp);
-    } else {
-        if (head_dim == 128) hipLaunchKernelGGL((kv_pack_kernel<f16_t, 128>), grid, dim3(256), 0, stream, k, v, kv_tokens, kv_blocks, kp, vp);
-        else hipLaunchKernelGGL((kv_pack_kernel<f16_t, 64>), grid, dim3(256), 0, stream, k, v, kv_tokens, kv_blocks, kp, vp);
+template <typename T>
+int launch_attention_dt(int padded, bool sparse, bool tail, const AttnArgs& a, int bh_count, hipStream_t stream) {
+    switch (padded) {
+        case 64: return launch_attention_d<T, 64>(sparse, tail, a, bh_count, stream);
+        case 96: return launch_attention_d<T, 96>(sparse, tail, a, bh_count, stream);
+        case 128: return launch_attention_d<T, 128>(sparse, tail, a, bh_count, stream);
+        case 160: return launch_attention_d<T, 160>(sparse, tail, a, bh_count, stream);
+        case 192: return launch_attention_d<T, 192>(sparse, tail, a, bh_count, stream);
+        case 256: return launch_attention_d<T, 256>(sparse, tail, a, bh_count, stream);
+        default: return pisa_host::fail(PISA_ERR_UNSUPPORTED, "attention kernel: padded head dim %d", padded);
     }
+}
+
+int launch_attention(int dtype, int padded, bool sparse, bool tail, const AttnArgs& a, int bh_count,
+                     hipStream_t stream) {
+    if (dtype == PISA_DTYPE_BF16) return launch_attention_dt<bf16_t>(padded, sparse, tail, a, bh_count, stream);
+    return launch_attention_dt<f16_t>(padded, sparse, tail, a, bh_count, stream);
+}
+
+template <typename T>
+int launch_kv_pack_t(int padded, int head_dim, const View& k, const View& v, TokenMap map, int kv_tokens,
+                     int kv_blocks, int bh_count, char* kp, char* vp, hipStream_t stream) {
+    const dim3 grid(bh_count * kv_blocks);
+#define PISA_KV_PACK(DP)                                                                                     \
+    case DP:                                                                                                 \
+        hipLaunchKernelGGL((kv_pack_kernel<T, DP>), grid, dim3(256), 0, stream, k, v, map, kv_tokens, kv_blocks, \
+                           head_dim, kp, vp);                                                                \
+        break;
+    switch (padded) {
+        PISA_KV_PACK(64)
+        PISA_KV_PACK(96)
+        PISA_KV_PACK(128)
+        PISA_KV_PACK(160)
+        PISA_KV_PACK(192)
+        PISA_KV_PACK(256)
+        default: return pisa_host::fail(PISA_ERR_UNSUPPORTED, "kv pack: padded head dim %d", padded);
+    }
+#undef PISA_KV_PACK
     return pisa_host::check_launch("kv_pack_kernel");
+}
+
+int launch_kv_pack(int dtype, int padded, int head_dim, const View& k, const View& v, TokenMap map, int kv_tokens,
+                   int kv_blocks, int bh_count, char* kp, char* vp, hipStream_t stream) {
+    if (dtype == PISA_DTYPE_BF16)
+        return launch_kv_pack_t<bf16_t>(padded, head_dim, k, v, map, kv_tokens, kv_blocks, bh_count, kp, vp, stream);
+    return launch_kv_pack_t<f16_t>(padded, head_dim, k, v, map, kv_tokens, kv_blocks, bh_count, kp, vp, stream);
 }
 
 }  // namespace pisa

@@ -7,9 +7,9 @@
 //     values A[col][slot] / B[slot][col] for the 16-deep contraction slots
 //     half*8 .. half*8+7, and receives accumulator values
 //       D[row = 8*(v/4) + 4*half + (v%4)][col],  v = 0..15;
-//   * key blocks are stored transposed ("V^T blocks", [D][64]) with the key
-//     index bit-permuted by swap23(), so that a lane's 8 accumulator rows of
-//     one MFMA output feed one 16-byte operand load of the next MFMA.
+//   * value blocks are stored as V^T operand fragments with the key index
+//     bit-permuted by swap23(), so that a lane's 8 accumulator rows of one
+//     MFMA output (probabilities) are the B operand of the next MFMA.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -123,6 +123,20 @@ __host__ __device__ __forceinline__ int kfrag_elem(int key, int d, int D) {
 __host__ __device__ __forceinline__ int vfrag_elem(int key, int d) {
     const int p = (key & ~12) | ((key & 4) << 1) | ((key & 8) >> 1);  // swap23(key)
     return ((((d >> 5) * 4 + (p >> 4)) * 64 + ((p >> 3) & 1) * 32 + (d & 31)) << 3) + (p & 7);
+}
+
+// Head dims other than 128 (generic path, dense attention) run on kernels
+// instantiated for a padded width: the packed tables hold zeros in dims
+// [D, Dp), queries are loaded as zero there and outputs are not stored.
+// Returns 0 for unsupported D (D must be a multiple of 8, at most 256).
+__host__ __device__ inline int padded_head_dim(int d) {
+    if (d <= 0 || d % 8 || d > 256) return 0;
+    if (d <= 64) return 64;
+    if (d <= 96) return 96;
+    if (d <= 128) return 128;
+    if (d <= 160) return 160;
+    if (d <= 192) return 192;
+    return 256;
 }
 
 // ---------------------------------------------------------------- views

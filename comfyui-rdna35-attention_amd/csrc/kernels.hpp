@@ -27,6 +27,7 @@ struct StatsArgs {
     void* kbar_pad;    // [BH][npad/64] packed key chunks of dtype k_bar
     void* vbar_t_pad;  // [BH][npad/64] packed value chunks of dtype v_bar
     int npad;
+    int head_dim;      // real head dim D (outputs are [.][.][D]; packed tables use the padded width)
 };
 
 // Sums the per-chunk partials in chunk order; writes H_sum (fp32), the
@@ -74,6 +75,7 @@ struct AttnArgs {
     // first-order correction
     const char* ht;          // [BH] packed D x D (kfrag_elem), element (c, r) = H_sum[r][c]
     float corr_scale;        // s / T
+    int head_dim;            // real head dim (<= the kernel's padded width)
 };
 
 struct LayoutArgs {
@@ -87,10 +89,15 @@ struct LayoutArgs {
 int launch_stats(int dtype, int mode, const StatsArgs& a, int bh_count, hipStream_t stream);
 int launch_stats_reduce(int dtype, const ReduceArgs& a, int bh_count, hipStream_t stream);
 int launch_route(const RouteArgs& a, hipStream_t stream);
-int launch_attention(int dtype, int head_dim, bool sparse, bool tail, const AttnArgs& a, int bh_count,
+// Block means for the generic path at padded width `padded` (a.head_dim < 128 or > 128).
+int launch_stats_means(int dtype, int padded, const StatsArgs& a, int bh_count, hipStream_t stream);
+// `padded` = padded_head_dim(a.head_dim); dense (sparse = tail = false) or PISA (both true).
+int launch_attention(int dtype, int padded, bool sparse, bool tail, const AttnArgs& a, int bh_count,
                      hipStream_t stream);
-int launch_kv_pack(int dtype, int head_dim, const View& k, const View& v, int kv_tokens, int kv_blocks, int bh_count,
-                   char* kp, char* vp, hipStream_t stream);
+// Packed key / value blocks of width `padded` (dims >= head_dim and rows >= kv_tokens are zero);
+// block j row r is token map(64 j + r).
+int launch_kv_pack(int dtype, int padded, int head_dim, const View& k, const View& v, TokenMap map, int kv_tokens,
+                   int kv_blocks, int bh_count, char* kp, char* vp, hipStream_t stream);
 int launch_fixed_block(int dtype, int head_dim, const View& q, const View& k, const View& v, const OutView& o,
                        int tokens, int bh_count, float scale, int causal, hipStream_t stream);
 int launch_pack(int dtype, const LayoutArgs& a, int bh_count, hipStream_t stream);

@@ -327,6 +327,118 @@ __global__ __launch_bounds__(256) void stats_reduce_kernel(ReduceArgs a) {
     }
 }
 
+// Block means of the generic path at head dims other than 128 (the
+// reference uses the first-order term only at 128, generic_pisa.py:332, so
+// no H_sum is formed): one 256-thread workgroup per (batch*head, block).
+// Thread (row group rr, piece pc) sums the 8 dims pc*8.. of rows rr, rr+R, ..
+// in fp32; an LDS pass adds the R row groups in order, and means are
+// sum / len (generic_pisa.py:128-132, pisa_kernel.py:72-77).  Writes the
+// [BH][N][D] means and the packed centroid chunks at the padded width DP
+// (zero in dims >= D and for the centroids past the last block).
+template <typename T, int DP>
+__global__ __launch_bounds__(256) void stats_means_kernel(StatsArgs a) {
+    typedef typename Elem<T>::vec8 vec8;
+    constexpr int P = DP / 8;    // 16-byte pieces per row
+    constexpr int R = 256 / P;   // rows per pass
+    constexpr int kPasses = (kBlock + R - 1) / R;
+    __shared__ float red[3][R][DP];
+    const int t = threadIdx.x;
+    const int bh = blockIdx.x / a.blocks;
+    const int b = blockIdx.x - bh * a.blocks;
+    const int start = b * kBlock;
+    const int len = min(kBlock, a.tokens - start);
+    const int pc = t % P;
+    const int rr = t / P;
+    const bool mapped = t < R * P;
+    float sq[8], sk[8], sv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sq[e] = sk[e] = sv[e] = 0.0f;
+    if (mapped && pc * 8 < a.head_dim) {
+        const int64_t off = pc * 8 * (int64_t)sizeof(T);
+#pragma unroll
+        for (int pass = 0; pass < kPasses; ++pass) {
+            const int r = pass * R + rr;
+            if (r < len) {
+                const int raster = a.map(start + r);
+                const vec8 x = load8<vec8>(a.q.data + a.q.row(bh, raster) * sizeof(T) + off);
+                const vec8 y = load8<vec8>(a.k.data + a.k.row(bh, raster) * sizeof(T) + off);
+                const vec8 z = load8<vec8>(a.v.data + a.v.row(bh, raster) * sizeof(T) + off);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    sq[e] += to_f32(x[e]);
+                    sk[e] += to_f32(y[e]);
+                    sv[e] += to_f32(z[e]);
+                }
+            }
+        }
+    }
+    if (mapped) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            red[0][rr][pc * 8 + e] = sq[e];
+            red[1][rr][pc * 8 + e] = sk[e];
+            red[2][rr][pc * 8 + e] = sv[e];
+        }
+    }
+    __syncthreads();
+    if (t >= DP) return;
+    const int d = t;
+    float mq = 0.0f, mk = 0.0f, mv = 0.0f;
+    for (int i = 0; i < R; ++i) {
+        mq += red[0][i][d];
+        mk += red[1][i][d];
+        mv += red[2][i][d];
+    }
+    const float fl = static_cast<float>(len);
+    mq /= fl;
+    mk /= fl;
+    mv /= fl;
+    const bool live = d < a.head_dim;
+    if (live) {
+        const int64_t o = ((int64_t)bh * a.blocks + b) * a.head_dim + d;
+        if (a.qc_f32) static_cast<float*>(a.qc_out)[o] = mq;
+        else static_cast<T*>(a.qc_out)[o] = from_f32<T>(mq);
+        a.kc_out[o] = mk;
+        if (a.vm_f32) static_cast<float*>(a.vm_out)[o] = mv;
+        else static_cast<T*>(a.vm_out)[o] = from_f32<T>(mv);
+        if (a.qc_route) a.qc_route[o] = mq;
+    }
+    const int64_t head_base = (int64_t)bh * a.npad * DP;
+    T* kbar = static_cast<T*>(a.kbar_pad);
+    T* vbar = static_cast<T*>(a.vbar_t_pad);
+    const int64_t chunk_base = head_base + (int64_t)(b & ~63) * DP;
+    kbar[chunk_base + kfrag_elem(b & 63, d, DP)] = live ? from_f32<T>(mk) : T(0.0f);
+    vbar[chunk_base + vfrag_elem(b & 63, d)] = live ? from_f32<T>(mv) : T(0.0f);
+    if (b == a.blocks - 1) {
+        // centroids past the last block: masked to -inf in the tail, zero here
+        // so that 0 * value stays finite in the PV product
+        for (int j = a.blocks; j < a.npad; ++j) {
+            const int64_t base = head_base + (int64_t)(j & ~63) * DP;
+            kbar[base + kfrag_elem(j & 63, d, DP)] = T(0.0f);
+            vbar[base + vfrag_elem(j & 63, d)] = T(0.0f);
+        }
+    }
+}
+
+template <typename T>
+int launch_stats_means_t(int padded, const StatsArgs& a, int bh_count, hipStream_t stream) {
+    const dim3 grid(bh_count * a.blocks);
+    switch (padded) {
+        case 64: hipLaunchKernelGGL((stats_means_kernel<T, 64>), grid, dim3(256), 0, stream, a); break;
+        case 96: hipLaunchKernelGGL((stats_means_kernel<T, 96>), grid, dim3(256), 0, stream, a); break;
+        case 160: hipLaunchKernelGGL((stats_means_kernel<T, 160>), grid, dim3(256), 0, stream, a); break;
+        case 192: hipLaunchKernelGGL((stats_means_kernel<T, 192>), grid, dim3(256), 0, stream, a); break;
+        case 256: hipLaunchKernelGGL((stats_means_kernel<T, 256>), grid, dim3(256), 0, stream, a); break;
+        default: return pisa_host::fail(PISA_ERR_UNSUPPORTED, "block means: padded head dim %d", padded);
+    }
+    return pisa_host::check_launch("stats_means_kernel");
+}
+
+int launch_stats_means(int dtype, int padded, const StatsArgs& a, int bh_count, hipStream_t stream) {
+    if (dtype == PISA_DTYPE_BF16) return launch_stats_means_t<bf16_t>(padded, a, bh_count, stream);
+    return launch_stats_means_t<f16_t>(padded, a, bh_count, stream);
+}
+
 template <typename T, int MODE>
 int launch_stats_t(const StatsArgs& a, int bh_count, hipStream_t stream) {
     hipLaunchKernelGGL((stats_kernel<T, MODE>), dim3(bh_count * a.chunks), dim3(kStatsThreads), 0,

@@ -31,6 +31,7 @@ __version__ = "1.0.0"
 
 BLOCK_SIZE = 64
 HEAD_DIM = 128
+GENERIC_HEAD_DIMS = tuple(range(8, 257, 8))  # generic PISA (no first-order term off 128) and dense attention
 MAX_BLOCKS = 1024
 MAX_TOKENS = BLOCK_SIZE * MAX_BLOCKS
 SPATIAL_SIDE = 96
@@ -535,9 +536,9 @@ def capabilities() -> dict[str, object]:
         "spatial_sparse_exact_blocks": (SPATIAL_SPARSE_EXACT_BLOCKS,),
         "hyd_stats_head_dims": (HEAD_DIM,),
         "hyd_stats_dtypes": (torch.bfloat16, torch.float16),
-        "generic_head_dims": (HEAD_DIM,),
+        "generic_head_dims": GENERIC_HEAD_DIMS,
         "generic_dtypes": (torch.bfloat16, torch.float16),
-        "dense_head_dims": (64, 128),
+        "dense_head_dims": GENERIC_HEAD_DIMS,
         "fixed_block_head_dims": (32, 64, 128),
         "fixed_block_dtypes": (torch.bfloat16, torch.float16, torch.float32),
     }

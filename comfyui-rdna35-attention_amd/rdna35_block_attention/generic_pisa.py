@@ -28,7 +28,10 @@ from . import diagnostics
 BLOCK_SIZE = 64
 MIN_TOKENS = 8192
 SPATIAL_BLOCK_EDGE = 8
-SUPPORTED_HEAD_DIMS = (128,)
+# Head dims the HIP kernels take (multiples of 8 up to 256; dims are padded to
+# 64/96/128/160/192/256 inside).  The first-order term runs at 128 bf16 only,
+# as in the reference (generic_pisa.py:332).
+SUPPORTED_HEAD_DIMS = tuple(range(8, 257, 8))
 
 
 # ----------------------------------------------------------------------------- tile permutations

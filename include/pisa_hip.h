@@ -128,6 +128,9 @@ PISA_HIP_EXPORT int64_t pisa_hip_forward_workspace_bytes(int32_t batch, int32_t 
  * spatial variant (_forward_spatial_bhtd_op, __init__.py:344-365, with the
  * fused epilogue of pisa_kernels.cu:296-340) and generic_pisa_attention
  * (generic_pisa.py:141-232).
+ *   head_dim       128, or any multiple of 8 up to 256 with PISA_STATS_GENERIC,
+ *                  PISA_ROUTE_CENTROID and first_order 0 (generic_pisa.py:332-333
+ *                  uses the first-order term only at 128 bf16)
  *   stats_mode     PISA_STATS_HYD or PISA_STATS_GENERIC
  *   route_mode     PISA_ROUTE_HYD or PISA_ROUTE_CENTROID
  *   first_order    1 adds C = s/T * q . bf16(H_sum) weighted by the tail mass
@@ -240,7 +243,8 @@ PISA_HIP_EXPORT int64_t attn_hip_dense_workspace_bytes(int32_t batch, int32_t he
 /*
  * Exact non-causal softmax attention, online softmax in fp32 on bf16/fp16
  * MFMA.  q/out have q_tokens rows, k/v kv_tokens rows (cross attention
- * allowed); any strides (unit head_dim stride).  head_dim 64 or 128.
+ * allowed); any strides (unit head_dim stride).  head_dim a multiple of 8
+ * up to 256 (the reference's Triton kernel takes 64 and 128).
  * Replaces full_attention_triton_bh (triton_kernel.py:113-197) and the dense
  * SDPA fallbacks of __init__.py:251-252.
  */

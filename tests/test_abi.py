@@ -64,6 +64,13 @@ def test_workspace_sizes(lib):
     assert lib.LIB.pisa_hip_forward_workspace_bytes(0, 16, 9216, 128, 23) == 0
     assert lib.LIB.attn_hip_dense_workspace_bytes(2, 16, 512, 128) == 2 * (2 * 16 * 512 * 128 * 2)
     assert lib.LIB.attn_hip_dense_workspace_bytes(1, 1, 65, 64) == 2 * (128 * 64 * 2)
+    # other head dims: packed tables at the padded width (40 -> 64, 80 -> 96, 160 -> 160, 200 -> 256)
+    for d, dp in ((40, 64), (80, 96), (160, 160), (200, 256), (8, 64)):
+        assert lib.LIB.attn_hip_dense_workspace_bytes(1, 2, 128, d) == 2 * (2 * 128 * dp * 2)
+    # generic PISA off 128 has no H_sum partials: smaller than at 128 despite the padding of 80 -> 96
+    assert lib.LIB.pisa_hip_forward_workspace_bytes(1, 4, 8192, 80, 32) < \
+        lib.LIB.pisa_hip_forward_workspace_bytes(1, 4, 8192, 128, 32)
+    assert lib.LIB.pisa_hip_forward_workspace_bytes(1, 4, 8192, 80, 32) > 2 * (4 * 8192 * 96 * 2)
 
 
 def _views(lib):
@@ -83,7 +90,13 @@ def test_forward_validation_rejects_before_any_launch(lib):
                                         over.get("grid", grid), a["exact"], a["scale"], a["sink"], a["stats"],
                                         a["route"], a["first"], None, None, None, 0, None)
 
-    assert call(head_dim=64) == 2                      # unsupported head_dim
+    assert call(head_dim=64) == 2                      # HYD statistics / first order only at 128
+    generic = dict(stats=lib.STATS_GENERIC, route=lib.ROUTE_CENTROID, first=0)
+    assert call(head_dim=100, **generic) == 2          # not a multiple of 8
+    assert call(head_dim=264, **generic) == 2          # above 256
+    assert call(head_dim=64, **{**generic, "first": 1}) == 2   # no first-order term off 128
+    assert call(head_dim=64, **{**generic, "route": lib.ROUTE_HYD}) == 2
+    assert call(head_dim=64, **generic) == 3           # supported: fails only for the missing workspace
     assert call(dtype=2) == 2                          # fp32 not supported by PISA
     assert call(exact=144) == 1                        # dense goes to attn_hip_dense_forward
     assert call(exact=0, sink=0) == 1                  # sink needs an exact block
@@ -97,7 +110,8 @@ def test_forward_validation_rejects_before_any_launch(lib):
 
 def test_other_entry_points_validate(lib):
     q, k, v, o = _views(lib)
-    assert lib.LIB.attn_hip_dense_forward(0, 1, 1, 64, 64, 96, q, k, v, o, 0.1, None, 0, None) == 2
+    assert lib.LIB.attn_hip_dense_forward(0, 1, 1, 64, 64, 100, q, k, v, o, 0.1, None, 0, None) == 2
+    assert lib.LIB.attn_hip_dense_forward(0, 1, 1, 64, 64, 264, q, k, v, o, 0.1, None, 0, None) == 2
     assert lib.LIB.attn_hip_fixed_block_forward(0, 1, 1, 64, 48, 64, q, k, v, o, 0.1, 0, None) == 2
     assert lib.LIB.attn_hip_fixed_block_forward(0, 1, 1, 64, 64, 32, q, k, v, o, 0.1, 0, None) == 2
     assert lib.LIB.pisa_hip_route_topk(1, 2000, 128, None, None, None, 1, 0.1, -2, 3, None, None, None) == 2

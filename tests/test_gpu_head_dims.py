@@ -1,0 +1,97 @@
+"""Head dims other than 128 on the MI355X: generic PISA without the
+first-order term (generic_pisa.py:332-333) and dense attention, against the
+numpy oracle.  The kernels run at a padded width (64/96/128/160/192/256)
+with zero dims in the packed tables; these tests cover every padded width,
+both dtypes, raster and video token grids and short last blocks."""
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+from helpers import assert_close, np32, packed_to_merged, spatial_to_packed
+from oracle import attention as oatt
+from oracle import pisa as opisa
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float16: 2e-2, torch.bfloat16: 5e-2}
+
+
+@pytest.fixture(scope="module")
+def native():
+    import mi355x_pisa
+
+    return mi355x_pisa
+
+
+@pytest.mark.parametrize("head_dim,dtype,tokens,exact", [
+    (40, torch.float16, 1000, 4),     # SD1.5 widths (tests/test_generic_pisa.py:93-99)
+    (80, torch.float16, 1024, 4),
+    (160, torch.float16, 777, 3),
+    (64, torch.bfloat16, 1024, 5),    # SDXL / LTX
+    (64, torch.float16, 640, 10),
+    (96, torch.bfloat16, 900, 2),
+    (192, torch.bfloat16, 512, 2),
+    (256, torch.float16, 512, 3),
+    (128, torch.float16, 1024, 4),    # fp16 at 128: no first-order term either
+])
+def test_generic_forward_head_dims_match_oracle(native, head_dim, dtype, tokens, exact):
+    gen = torch.Generator().manual_seed(head_dim * 1000 + tokens)
+    bh = 3
+    q4, k4, v4 = (torch.randn((1, bh, tokens, head_dim), generator=gen).to(dtype).cuda() for _ in range(3))
+    s = 1 / math.sqrt(head_dim)
+    print(f"generic D={head_dim} {dtype} T={tokens} exact={exact}", flush=True)
+    out = native.generic_forward(q4, k4, v4, exact, s, False)
+    name = "bf16" if dtype == torch.bfloat16 else "f16"
+    ref = opisa.generic_forward(*(np32(t).reshape(bh, tokens, head_dim) for t in (q4, k4, v4)), exact, s,
+                                first_order=False, dtype=name)
+    expected = ref.reshape(1, bh, tokens, head_dim).transpose(0, 2, 1, 3)
+    assert out.shape == (1, tokens, bh, head_dim)
+    assert_close(np32(out), expected, TOL[dtype], TOL[dtype], f"generic D={head_dim}")
+
+
+@pytest.mark.parametrize("head_dim,grid", [(80, (2, 16, 32)), (64, (1, 32, 32)), (160, (1, 24, 32))])
+def test_generic_forward_head_dims_on_token_grids(native, head_dim, grid):
+    tokens = math.prod(grid)
+    gen = torch.Generator().manual_seed(head_dim + tokens)
+    q4, k4, v4 = (torch.randn((1, 2, tokens, head_dim), generator=gen).to(torch.float16).cuda() for _ in range(3))
+    exact = 3
+    out = native.generic_forward(q4, k4, v4, exact, 1 / math.sqrt(head_dim), False, token_grid=grid)
+    packed = [spatial_to_packed(t, *grid) for t in (q4, k4, v4)]
+    ref = opisa.generic_forward(*packed, exact, first_order=False, dtype="f16")
+    expected = packed_to_merged(ref, 1, 2, *grid)
+    assert_close(np32(out).reshape(1, tokens, 2 * head_dim), expected, 2e-2, 2e-2, f"grid D={head_dim}")
+
+
+def test_first_order_is_refused_off_128(native):
+    q = torch.randn((1, 1, 512, 64), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(RuntimeError, match="first-order"):
+        native.generic_forward(q, q, q, 2, 0.125, True)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("q_tokens,kv_tokens,head_dim", [
+    (100, 130, 40), (64, 257, 80), (77, 64, 160), (130, 190, 192), (65, 99, 256), (33, 700, 96), (129, 64, 8),
+])
+def test_dense_head_dims_match_oracle(native, dtype, q_tokens, kv_tokens, head_dim):
+    gen = torch.Generator().manual_seed(q_tokens * 7 + kv_tokens + head_dim)
+    q = torch.randn((2, 2, q_tokens, head_dim), generator=gen).to(dtype).cuda()
+    k = torch.randn((2, 2, kv_tokens, head_dim), generator=gen).to(dtype).cuda()
+    v = torch.randn((2, 2, kv_tokens, head_dim), generator=gen).to(dtype).cuda()
+    print(f"dense D={head_dim} {dtype} Tq={q_tokens} Tk={kv_tokens}", flush=True)
+    out = native.dense_attention(q, k, v, 1 / math.sqrt(head_dim))
+    expected = oatt.dense_attention(np32(q), np32(k), np32(v))
+    assert_close(np32(out), expected, TOL[dtype], TOL[dtype], f"dense D={head_dim}")
+
+
+def test_dense_head_dim_strided_merged_output(native):
+    """SD1.5-style [B,T,H*D] storage read as BHTD views, merged output (the ComfyUI layout)."""
+    batch, tokens, heads, head_dim = 1, 300, 8, 40
+    gen = torch.Generator().manual_seed(40)
+    x = torch.randn((3, batch, tokens, heads * head_dim), generator=gen).to(torch.float16).cuda()
+    q, k, v = (t.view(batch, tokens, heads, head_dim).transpose(1, 2) for t in x)
+    out = native.dense_attention(q, k, v, 1 / math.sqrt(head_dim), merged_output=True)
+    expected = oatt.dense_attention(np32(q), np32(k), np32(v)).transpose(0, 2, 1, 3).reshape(batch, tokens, -1)
+    assert_close(np32(out), expected, 2e-2, 2e-2, "dense merged D=40")
