@@ -172,6 +172,33 @@ def test_generic_override_on_video_grid():
     assert_close(np32(out), expected, 5e-2, 5e-2, "generic video override")
 
 
+@pytest.mark.parametrize("head_dim,dtype", [(40, torch.float16), (80, torch.float16), (160, torch.float16),
+                                             (64, torch.bfloat16)])
+def test_generic_override_sd_head_dims(head_dim, dtype):
+    """SD1.5 / SDXL-style flattened self-attention (tests/test_generic_pisa.py:93-125 profiles) on the HIP path:
+    no first-order term and a budget of at least 0.25 off 128 bf16 (generic_pisa.py:332-333)."""
+    from rdna35_block_attention.generic_pisa import make_generic_pisa_override
+    from rdna35_block_attention.pisa_runtime import PISARuntimeState
+
+    heads, tokens = 2, 8192
+    gen = torch.Generator().manual_seed(head_dim)
+    merged = [torch.randn((1, tokens, heads * head_dim), generator=gen).to(dtype).cuda() for _ in range(3)]
+    state = PISARuntimeState(armed=True)
+    override = make_generic_pisa_override(exact_budget=0.15625, device_index=torch.cuda.current_device(),
+                                          previous_override=None, runtime_state=state)
+    out = override(lambda *a, **kw: "original", *merged, heads, is_self_attention=True, transformer_options={})
+    assert state.backend_counts["hip_generic_0th"] == 1, state.report()
+    assert out.shape == (1, tokens, heads * head_dim)
+    bhtd = [np32(t).reshape(1, tokens, heads, head_dim).transpose(0, 2, 1, 3).reshape(heads, tokens, head_dim)
+            for t in merged]
+    exact = math.ceil(0.25 * (tokens // 64))  # budget raised to 0.25
+    name = "bf16" if dtype == torch.bfloat16 else "f16"
+    ref = opisa.generic_forward(*bhtd, exact, first_order=False, dtype=name)
+    expected = ref.reshape(1, heads, tokens, head_dim).transpose(0, 2, 1, 3).reshape(1, tokens, heads * head_dim)
+    tol = 2e-2 if dtype == torch.float16 else 5e-2
+    assert_close(np32(out), expected, tol, tol, f"generic override D={head_dim}")
+
+
 def test_h3_override_reads_strided_views():
     from rdna35_block_attention.minimax_h3_attention import make_minimax_h3_attention_override
 
