@@ -667,9 +667,9 @@ int attn_hip_dense_forward(int32_t dtype, int32_t batch, int32_t heads, int32_t 
     return pisa::launch_attention(dtype, padded, false, false, aa, bh, st);
 }
 
-int attn_hip_fixed_block_forward(int32_t dtype, int32_t batch, int32_t heads, int32_t tokens, int32_t head_dim,
-                                 int32_t block_size, pisa_view q, pisa_view k, pisa_view v, pisa_view out, float scale,
-                                 int32_t causal, void* stream) {
+int attn_hip_fixed_block_forward_masked(int32_t dtype, int32_t batch, int32_t heads, int32_t tokens,
+                                        int32_t head_dim, int32_t block_size, pisa_view q, pisa_view k, pisa_view v,
+                                        pisa_view out, float scale, int32_t causal, pisa_mask mask, void* stream) {
     if (dtype != PISA_DTYPE_BF16 && dtype != PISA_DTYPE_F16 && dtype != PISA_DTYPE_F32)
         return fail(PISA_ERR_UNSUPPORTED, "fixed-block attention supports bf16, fp16 and fp32");
     if (batch <= 0 || heads <= 0 || tokens <= 0) return fail(PISA_ERR_INVALID_ARGUMENT, "requires B>0, H>0, T>0");
@@ -678,15 +678,41 @@ int attn_hip_fixed_block_forward(int32_t dtype, int32_t batch, int32_t heads, in
         return fail(PISA_ERR_UNSUPPORTED, "fixed-block attention supports head_dim 32/64/128, got %d", head_dim);
     if (!(scale == scale) || scale == __builtin_inff() || scale == -__builtin_inff())
         return fail(PISA_ERR_INVALID_ARGUMENT, "scale must be finite");
+    if (mask.kind < PISA_MASK_NONE || mask.kind > PISA_MASK_ADD_BF16)
+        return fail(PISA_ERR_INVALID_ARGUMENT, "unknown mask kind %d", mask.kind);
+    if (mask.kind != PISA_MASK_NONE) {
+        const int esize = mask.kind == PISA_MASK_BOOL ? 1 : mask.kind == PISA_MASK_ADD_F32 ? 4 : 2;
+        if (!mask.data || (reinterpret_cast<uintptr_t>(mask.data) & (esize - 1)))
+            return fail(PISA_ERR_INVALID_ARGUMENT, "mask data must be non-null and aligned to its element size");
+        if (mask.heads <= 0 || batch * heads % mask.heads)
+            return fail(PISA_ERR_INVALID_ARGUMENT, "mask heads %d must divide B*H=%d", mask.heads, batch * heads);
+    }
     const int es = elem_size(dtype);
     int rc;
     if ((rc = check_view("q", q, es, false)) || (rc = check_view("k", k, es, false)) ||
         (rc = check_view("v", v, es, false)) || (rc = check_view("out", out, es, false)))
         return rc;
     if ((rc = check_device())) return rc;
+    pisa::MaskView mv;
+    mv.data = static_cast<const char*>(mask.data);
+    mv.kind = mask.kind;
+    mv.heads = mask.kind != PISA_MASK_NONE ? mask.heads : 1;
+    mv.sb = mask.batch_stride;
+    mv.sh = mask.head_stride;
+    mv.sq = mask.query_stride;
+    mv.sk = mask.key_stride;
     return pisa::launch_fixed_block(dtype, head_dim, to_view(q, heads), to_view(k, heads), to_view(v, heads),
-                                    to_out(out, heads), tokens, batch * heads, scale, causal ? 1 : 0,
+                                    to_out(out, heads), tokens, batch * heads, scale, causal ? 1 : 0, mv,
                                     static_cast<hipStream_t>(stream));
+}
+
+int attn_hip_fixed_block_forward(int32_t dtype, int32_t batch, int32_t heads, int32_t tokens, int32_t head_dim,
+                                 int32_t block_size, pisa_view q, pisa_view k, pisa_view v, pisa_view out, float scale,
+                                 int32_t causal, void* stream) {
+    pisa_mask none;
+    memset(&none, 0, sizeof(none));
+    return attn_hip_fixed_block_forward_masked(dtype, batch, heads, tokens, head_dim, block_size, q, k, v, out, scale,
+                                               causal, none, stream);
 }
 
 }  // extern "C"

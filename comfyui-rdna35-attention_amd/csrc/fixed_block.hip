@@ -12,16 +12,30 @@
 // fixed_block_attention_ref (reference.py:179-198: fp32 scores, softmax, fp32
 // P @ V, cast to the input dtype).  Keys past the end of a partial last block
 // are excluded and `causal` masks keys after the query inside the block
-// (reference.py:186-188, triton_kernel.py:86-89).
+// (reference.py:186-188, triton_kernel.py:86-89); an attention mask then
+// removes keys (bool, false -> -inf) or adds to the scaled scores
+// (reference.py:190-195).  A row with every key masked gives NaN, the value
+// torch.softmax returns for it.
 #include "kernels.hpp"
 
 namespace pisa {
 
 template <typename T> __device__ __forceinline__ float ld(const char* p) { return to_f32(*reinterpret_cast<const T*>(p)); }
 
+// Score after the attention mask entry at element offset `off`.
+__device__ __forceinline__ float apply_mask(const MaskView& m, int64_t off, float s) {
+    switch (m.kind) {
+        case PISA_MASK_BOOL: return m.data[off] ? s : -__builtin_inff();
+        case PISA_MASK_ADD_F32: return s + reinterpret_cast<const float*>(m.data)[off];
+        case PISA_MASK_ADD_F16: return s + to_f32(reinterpret_cast<const f16_t*>(m.data)[off]);
+        case PISA_MASK_ADD_BF16: return s + to_f32(reinterpret_cast<const bf16_t*>(m.data)[off]);
+        default: return s;
+    }
+}
+
 template <typename T, int D>
 __global__ __launch_bounds__(256) void fixed_block_kernel(View q, View k, View v, OutView o, int tokens,
-                                                          int nblocks, float scale, int causal) {
+                                                          int nblocks, float scale, int causal, MaskView mask) {
     constexpr int kRow = D + 4;
     constexpr int kPRow = 68;
     __shared__ __attribute__((aligned(16))) float qs[64 * kRow];
@@ -72,6 +86,13 @@ __global__ __launch_bounds__(256) void fixed_block_kernel(View q, View k, View v
                 for (int j = 0; j < 4; ++j) s[i][j] = fmaf(qa[i][e], kb[j][e], s[i][j]);
     }
 
+    // mask element (b, h, start + row, start + key) of this workgroup's rows
+    int64_t mask_base = 0;
+    if (mask.kind != PISA_MASK_NONE) {
+        const int mb = bh / mask.heads;
+        const int mh = bh - mb * mask.heads;
+        mask_base = mb * mask.sb + mh * mask.sh + (int64_t)start * (mask.sq + mask.sk);
+    }
     float p[4][4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -80,8 +101,10 @@ __global__ __launch_bounds__(256) void fixed_block_kernel(View q, View k, View v
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int key = kt + 16 * j;
-            const bool dead = key >= len || (causal && key > row);
+            const bool dead = key >= len || row >= len || (causal && key > row);
             s[i][j] = dead ? -__builtin_inff() : s[i][j] * scale;
+            if (!dead && mask.kind != PISA_MASK_NONE)
+                s[i][j] = apply_mask(mask, mask_base + row * mask.sq + key * mask.sk, s[i][j]);
             mx = fmaxf(mx, s[i][j]);
         }
 #pragma unroll
@@ -95,7 +118,7 @@ __global__ __launch_bounds__(256) void fixed_block_kernel(View q, View k, View v
         }
 #pragma unroll
         for (int off = 1; off < 16; off <<= 1) sum += __shfl_xor(sum, off);
-        const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
+        const float inv = sum > 0.0f ? 1.0f / sum : __builtin_nanf("");  // all keys masked
 #pragma unroll
         for (int j = 0; j < 4; ++j) p[i][j] *= inv;
     }
@@ -134,23 +157,28 @@ __global__ __launch_bounds__(256) void fixed_block_kernel(View q, View k, View v
 
 template <typename T>
 int launch_fixed_t(int head_dim, const View& q, const View& k, const View& v, const OutView& o, int tokens,
-                   int bh_count, float scale, int causal, hipStream_t stream) {
+                   int bh_count, float scale, int causal, const MaskView& mask, hipStream_t stream) {
     const int nblocks = (tokens + 63) / 64;
     const dim3 grid(bh_count * nblocks);
     if (head_dim == 32)
-        hipLaunchKernelGGL((fixed_block_kernel<T, 32>), grid, dim3(256), 0, stream, q, k, v, o, tokens, nblocks, scale, causal);
+        hipLaunchKernelGGL((fixed_block_kernel<T, 32>), grid, dim3(256), 0, stream, q, k, v, o, tokens, nblocks, scale,
+                           causal, mask);
     else if (head_dim == 64)
-        hipLaunchKernelGGL((fixed_block_kernel<T, 64>), grid, dim3(256), 0, stream, q, k, v, o, tokens, nblocks, scale, causal);
+        hipLaunchKernelGGL((fixed_block_kernel<T, 64>), grid, dim3(256), 0, stream, q, k, v, o, tokens, nblocks, scale,
+                           causal, mask);
     else
-        hipLaunchKernelGGL((fixed_block_kernel<T, 128>), grid, dim3(256), 0, stream, q, k, v, o, tokens, nblocks, scale, causal);
+        hipLaunchKernelGGL((fixed_block_kernel<T, 128>), grid, dim3(256), 0, stream, q, k, v, o, tokens, nblocks, scale,
+                           causal, mask);
     return pisa_host::check_launch("fixed_block_kernel");
 }
 
 int launch_fixed_block(int dtype, int head_dim, const View& q, const View& k, const View& v, const OutView& o,
-                       int tokens, int bh_count, float scale, int causal, hipStream_t stream) {
-    if (dtype == PISA_DTYPE_BF16) return launch_fixed_t<bf16_t>(head_dim, q, k, v, o, tokens, bh_count, scale, causal, stream);
-    if (dtype == PISA_DTYPE_F16) return launch_fixed_t<f16_t>(head_dim, q, k, v, o, tokens, bh_count, scale, causal, stream);
-    return launch_fixed_t<float>(head_dim, q, k, v, o, tokens, bh_count, scale, causal, stream);
+                       int tokens, int bh_count, float scale, int causal, const MaskView& mask, hipStream_t stream) {
+    if (dtype == PISA_DTYPE_BF16)
+        return launch_fixed_t<bf16_t>(head_dim, q, k, v, o, tokens, bh_count, scale, causal, mask, stream);
+    if (dtype == PISA_DTYPE_F16)
+        return launch_fixed_t<f16_t>(head_dim, q, k, v, o, tokens, bh_count, scale, causal, mask, stream);
+    return launch_fixed_t<float>(head_dim, q, k, v, o, tokens, bh_count, scale, causal, mask, stream);
 }
 
 }  // namespace pisa

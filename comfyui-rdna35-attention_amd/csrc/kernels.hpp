@@ -98,8 +98,15 @@ int launch_attention(int dtype, int padded, bool sparse, bool tail, const AttnAr
 // block j row r is token map(64 j + r).
 int launch_kv_pack(int dtype, int padded, int head_dim, const View& k, const View& v, TokenMap map, int kv_tokens,
                    int kv_blocks, int bh_count, char* kp, char* vp, hipStream_t stream);
+// Fixed-block attention mask, broadcast to [B][heads][T][T] by element strides.
+struct MaskView {
+    const char* data;
+    int kind;  // PISA_MASK_*
+    int heads;
+    int64_t sb, sh, sq, sk;
+};
 int launch_fixed_block(int dtype, int head_dim, const View& q, const View& k, const View& v, const OutView& o,
-                       int tokens, int bh_count, float scale, int causal, hipStream_t stream);
+                       int tokens, int bh_count, float scale, int causal, const MaskView& mask, hipStream_t stream);
 int launch_pack(int dtype, const LayoutArgs& a, int bh_count, hipStream_t stream);
 int launch_unpack(int dtype, const char* packed, char* out, TokenMap map, int tokens, int head_dim, int heads,
                   int bh_count, hipStream_t stream);

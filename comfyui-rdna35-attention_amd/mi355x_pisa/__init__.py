@@ -22,6 +22,8 @@ from __future__ import annotations
 import math
 import struct
 
+from typing import Optional
+
 import torch
 
 from . import _lib
@@ -139,15 +141,30 @@ def _launch_dense(q4, k4, v4, out4, scale):
         )
 
 
-def _launch_fixed_block(q4, k4, v4, out4, scale, causal):
+_MASK_KINDS = {torch.bool: _lib.MASK_BOOL, torch.float32: _lib.MASK_ADD_F32, torch.float16: _lib.MASK_ADD_F16,
+               torch.bfloat16: _lib.MASK_ADD_BF16}
+
+
+def _mask_struct(mask: torch.Tensor | None) -> _lib.PisaMask:
+    """pisa_mask of a [B', H', T, T] view (0 strides broadcast; B' * H' = the kernel's B*H)."""
+    if mask is None:
+        return _lib.PisaMask(None, _lib.MASK_NONE, 1, 0, 0, 0, 0)
+    if mask.ndim != 4 or mask.dtype not in _MASK_KINDS:
+        raise ValueError("the fixed-block mask view must be 4-D bool/float32/float16/bfloat16")
+    sb, sh, sq, sk = mask.stride()
+    return _lib.PisaMask(mask.data_ptr(), _MASK_KINDS[mask.dtype], mask.shape[1], sb, sh, sq, sk)
+
+
+def _launch_fixed_block(q4, k4, v4, out4, scale, causal, mask=None):
     batch, heads, tokens, head_dim = q4.shape
     with torch.cuda.device(q4.device):
         check(
-            LIB.attn_hip_fixed_block_forward(
+            LIB.attn_hip_fixed_block_forward_masked(
                 dtype_code(q4.dtype), batch, heads, tokens, head_dim, BLOCK_SIZE,
-                view4(q4), view4(k4), view4(v4), view4(out4), scale, int(bool(causal)), stream_of(q4.device),
+                view4(q4), view4(k4), view4(v4), view4(out4), scale, int(bool(causal)), _mask_struct(mask),
+                stream_of(q4.device),
             ),
-            "attn_hip_fixed_block_forward",
+            "attn_hip_fixed_block_forward_masked",
         )
 
 
@@ -279,15 +296,16 @@ def _dense_attention_op_fake(q, k, v, scale, merged_output):
 
 
 @torch.library.custom_op("mi355x_pisa::fixed_block_attention", mutates_args=(), device_types="cuda")
-def _fixed_block_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float, causal: bool) -> torch.Tensor:
+def _fixed_block_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float, causal: bool,
+                    mask: Optional[torch.Tensor]) -> torch.Tensor:
     out = q.new_empty(q.shape)
-    _launch_fixed_block(q, k, v, out, scale, causal)
+    _launch_fixed_block(q, k, v, out, scale, causal, mask)
     return out
 
 
 @_fixed_block_op.register_fake
-def _fixed_block_op_fake(q, k, v, scale, causal):
-    del k, v, scale, causal
+def _fixed_block_op_fake(q, k, v, scale, causal, mask):
+    del k, v, scale, causal, mask
     return q.new_empty(q.shape)
 
 
@@ -402,9 +420,14 @@ def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: fl
 
 
 def fixed_block_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float,
-                          causal: bool = False) -> torch.Tensor:
-    """64-token block-diagonal attention of [B,H,T,D] q/k/v -> [B,H,T,D] contiguous."""
-    return _fixed_block_op(q, k, v, float(scale), bool(causal))
+                          causal: bool = False, mask: torch.Tensor | None = None) -> torch.Tensor:
+    """64-token block-diagonal attention of [B,H,T,D] q/k/v -> [B,H,T,D] contiguous.
+
+    mask: optional [B', H', T, T] view on q's device with B' * H' = B * H
+    (broadcast dims as 0 strides): bool keeps a score where True, a float mask
+    is added to the scaled scores (reference.py:186-195).
+    """
+    return _fixed_block_op(q, k, v, float(scale), bool(causal), mask)
 
 
 def route_topk(q_centroids: torch.Tensor, k_centroids: torch.Tensor, h_norm: torch.Tensor | None,

@@ -25,6 +25,11 @@ STATS_GENERIC = 2
 ROUTE_HYD = 0
 ROUTE_CENTROID = 1
 NO_SINK = -2
+MASK_NONE = 0
+MASK_BOOL = 1
+MASK_ADD_F32 = 2
+MASK_ADD_F16 = 3
+MASK_ADD_BF16 = 4
 
 _DTYPES = {torch.bfloat16: DTYPE_BF16, torch.float16: DTYPE_F16, torch.float32: DTYPE_F32}
 
@@ -35,6 +40,18 @@ class PisaView(ctypes.Structure):
         ("batch_stride", ctypes.c_int64),
         ("head_stride", ctypes.c_int64),
         ("token_stride", ctypes.c_int64),
+    ]
+
+
+class PisaMask(ctypes.Structure):
+    _fields_ = [
+        ("data", ctypes.c_void_p),
+        ("kind", ctypes.c_int32),
+        ("heads", ctypes.c_int32),
+        ("batch_stride", ctypes.c_int64),
+        ("head_stride", ctypes.c_int64),
+        ("query_stride", ctypes.c_int64),
+        ("key_stride", ctypes.c_int64),
     ]
 
 
@@ -98,6 +115,10 @@ _SIGNATURES = {
     "attn_hip_fixed_block_forward": (
         ctypes.c_int,
         [_i32, _i32, _i32, _i32, _i32, _i32, PisaView, PisaView, PisaView, PisaView, _f32, _i32, _vp],
+    ),
+    "attn_hip_fixed_block_forward_masked": (
+        ctypes.c_int,
+        [_i32, _i32, _i32, _i32, _i32, _i32, PisaView, PisaView, PisaView, PisaView, _f32, _i32, PisaMask, _vp],
     ),
 }
 

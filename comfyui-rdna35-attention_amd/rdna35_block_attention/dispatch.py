@@ -6,7 +6,9 @@ auto, but the reason says the kernel was requested).  ``triton`` is accepted
 as an alias of ``hip`` so existing callers keep working.
 
 Eligible calls (ROCm device, fp32/fp16/bf16, head_dim 32/64/128,
-block_size 64, no mask, no autograd) always run the gfx950 kernel; a missing
+block_size 64, no autograd) always run the gfx950 kernel, attention masks
+included (the reference sends masked calls to its eager loop; the kernel
+applies the same 2-D/3-D/4-D masks, reference.py:114-156,186-195); a missing
 or failing HIP library raises instead of silently falling back.
 """
 from __future__ import annotations
@@ -16,7 +18,7 @@ from typing import Any
 import torch
 
 from . import diagnostics
-from .reference import fixed_block_attention_ref, normalize_qkv_to_bh_t_d
+from .reference import fixed_block_attention_ref, mask_view_bhtt, normalize_qkv_to_bh_t_d
 
 SUPPORTED_HEAD_DIMS = {32, 64, 128}
 SUPPORTED_DTYPES = {torch.float16, torch.bfloat16, torch.float32}
@@ -33,9 +35,9 @@ def _fallback(q, k, v, *, block_size, scale, causal, layout, heads, mask, reason
 def _hip_reject_reason(q_flat: torch.Tensor, k_flat: torch.Tensor, v_flat: torch.Tensor, *, block_size: int,
                        mask: torch.Tensor | None) -> str | None:
     """First reason the HIP kernel cannot take the call, in the reference's order (dispatch.py:50-79)."""
-    if mask is not None:
-        return "arbitrary_mask_uses_reference"
-    if any(t.requires_grad for t in (q_flat, k_flat, v_flat)):
+    if mask is not None and not isinstance(mask, torch.Tensor):
+        return "mask_is_not_a_tensor"
+    if any(t.requires_grad for t in (q_flat, k_flat, v_flat)) or (mask is not None and mask.requires_grad):
         return "requires_grad_uses_reference"
     if block_size != 64:
         return f"unsupported_block_size_{block_size}"
@@ -74,12 +76,15 @@ def fixed_block_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, 
     if reason is not None:
         return _fallback(q, k, v, reason=reason if mode == "auto" else f"requested_hip_but_{reason}", **common)
 
+    mask4 = None
+    if mask is not None:  # shape errors raise ValueError exactly as the eager loop would
+        mask4 = mask_view_bhtt(mask, batch_heads=q_flat.shape[0], info=info, device=q_flat.device)
     native = diagnostics.load_native()
     head_dim = info.head_dim
     s = float(scale) if scale is not None else head_dim ** -0.5
     out_flat = native.fixed_block_attention(q_flat.unsqueeze(1), k_flat.unsqueeze(1), v_flat.unsqueeze(1), s,
-                                            causal)[:, 0]
+                                            causal, mask4)[:, 0]
     out = info.restore(out_flat)
     details = {"backend": "hip", "fallback_reason": None, "optimized": True, "layout": info.layout,
-               "tokens": info.tokens, "head_dim": head_dim}
+               "tokens": info.tokens, "head_dim": head_dim, "mask": None if mask4 is None else str(mask4.dtype)}
     return (out, details) if return_diagnostics else out

@@ -90,6 +90,48 @@ def normalize_qkv_to_bh_t_d(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *
     return (to_flat(q), to_flat(k), to_flat(v), LayoutInfo(chosen, b, heads, t, d, restore))
 
 
+def mask_view_bhtt(mask: torch.Tensor, *, batch_heads: int, info: LayoutInfo,
+                   device: torch.device) -> torch.Tensor:
+    """The whole mask as a [B', H', T, T] broadcast view with B' * H' = BH, row bh = b' * H' + h'.
+
+    Same shape rules and errors as _mask_block (reference.py:114-156); this is
+    the view the HIP fixed-block kernel reads (zero strides for broadcast
+    dims), where the eager loop slices per block.  Masks that are neither
+    bool nor fp32/fp16/bf16 become fp32, the dtype they are added in.
+    """
+    m = mask.to(device=device)
+    if m.dtype != torch.bool and m.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+        m = m.to(torch.float32)
+    tokens = info.tokens
+    square = (tokens, tokens)
+    if m.ndim == 2:
+        if tuple(m.shape[-2:]) != square:
+            raise ValueError(f"2D mask must have shape [T,T], got {tuple(m.shape)}.")
+        return m.view(1, 1, tokens, tokens).expand(batch_heads, 1, tokens, tokens)
+    if m.ndim == 3:
+        if tuple(m.shape[-2:]) != square:
+            raise ValueError(f"3D mask must end with [T,T], got {tuple(m.shape)}.")
+        lead = m.shape[0]
+        if info.batch is not None and lead == info.batch:
+            return m.unsqueeze(1).expand(info.batch, info.heads, tokens, tokens)
+        if lead == 1:
+            return m.unsqueeze(1).expand(batch_heads, 1, tokens, tokens)
+        if lead == batch_heads:
+            return m.unsqueeze(1)
+        raise ValueError(f"3D mask batch dimension {lead} is not compatible with BH={batch_heads}.")
+    if m.ndim == 4:
+        if info.batch is None or info.heads is None:
+            raise ValueError("4D mask requires a layout with known B and H.")
+        if tuple(m.shape[-2:]) != square:
+            raise ValueError(f"4D mask must end with [T,T], got {tuple(m.shape)}.")
+        if m.shape[0] not in (1, info.batch):
+            raise ValueError(f"4D mask batch dimension {m.shape[0]} is not compatible with B={info.batch}.")
+        if m.shape[1] not in (1, info.heads):
+            raise ValueError(f"4D mask head dimension {m.shape[1]} is not compatible with H={info.heads}.")
+        return m.expand(info.batch, info.heads, tokens, tokens)
+    raise ValueError(f"Unsupported mask rank {m.ndim}.")
+
+
 def _mask_block(mask: torch.Tensor | None, start: int, end: int, *, batch_heads: int, info: LayoutInfo,
                 device: torch.device) -> torch.Tensor | None:
     """The [BH, n, n] slice of a 2-D/3-D/4-D attention mask for tokens [start, end)."""

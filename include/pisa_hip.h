@@ -100,6 +100,30 @@ typedef struct pisa_token_grid {
     int32_t width;
 } pisa_token_grid;
 
+/*
+ * Attention mask of fixed-block attention (fixed_block_attention_ref's
+ * `mask`, reference.py:114-156 slicing, :186-195 use), already broadcast to
+ * [B, H, T, T]: element (b, h, i, j) is at data + b*batch_stride +
+ * h*head_stride + i*query_stride + j*key_stride (elements; a stride of 0
+ * broadcasts), with h < heads.  Only the block-diagonal entries are read.
+ *   PISA_MASK_BOOL      1-byte values, the score is kept where nonzero
+ *   PISA_MASK_ADD_F32 / _F16 / _BF16   added to the scaled score
+ */
+#define PISA_MASK_NONE 0
+#define PISA_MASK_BOOL 1
+#define PISA_MASK_ADD_F32 2
+#define PISA_MASK_ADD_F16 3
+#define PISA_MASK_ADD_BF16 4
+typedef struct pisa_mask {
+    const void* data;
+    int32_t kind;
+    int32_t heads;
+    int64_t batch_stride;
+    int64_t head_stride;
+    int64_t query_stride;
+    int64_t key_stride;
+} pisa_mask;
+
 /* ---- library metadata -------------------------------------------------- */
 
 /* API revision of this header (the reference checks api==6, pisa_attention.py:470). */
@@ -264,6 +288,18 @@ PISA_HIP_EXPORT int attn_hip_fixed_block_forward(int32_t dtype, int32_t batch, i
                                  int32_t head_dim, int32_t block_size, pisa_view q, pisa_view k,
                                  pisa_view v, pisa_view out, float scale, int32_t causal,
                                  void* stream);
+
+/*
+ * attn_hip_fixed_block_forward with an attention mask (the masked calls the
+ * reference sends to its eager block loop, dispatch.py:50-79 ->
+ * fixed_block_attention_ref, reference.py:186-195): causal masking first,
+ * then the bool mask (-inf where false) or the additive mask; a row whose
+ * keys are all masked gives NaN, as torch.softmax does.
+ */
+PISA_HIP_EXPORT int attn_hip_fixed_block_forward_masked(int32_t dtype, int32_t batch, int32_t heads, int32_t tokens,
+                                        int32_t head_dim, int32_t block_size, pisa_view q, pisa_view k,
+                                        pisa_view v, pisa_view out, float scale, int32_t causal,
+                                        pisa_mask mask, void* stream);
 
 #ifdef __cplusplus
 }

@@ -27,11 +27,16 @@ def dense_attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float | 
 
 
 def fixed_block_attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, block_size: int = 64,
-                          scale: float | None = None, causal: bool = False, out_dtype: str = "f32") -> np.ndarray:
+                          scale: float | None = None, causal: bool = False, out_dtype: str = "f32",
+                          mask: np.ndarray | None = None) -> np.ndarray:
     """Block loop of fixed_block_attention_ref (reference.py:159-200) on [..., T, D] arrays.
 
     Each block of block_size tokens attends only to itself (the last block
     may be shorter); causal masks keys after the query inside the block.
+    `mask` ([..., T, T], broadcastable to q's leading axes) is applied after
+    the causal fill (reference.py:190-195): bool keeps a score where True
+    (-inf elsewhere), any other dtype is added to the scaled score.  A row
+    with every score -inf gives NaN, the value torch.softmax returns.
     Scores, softmax and P@V in float64; output rounded to out_dtype.
     """
     q64 = np.asarray(q, dtype=np.float64)
@@ -46,7 +51,15 @@ def fixed_block_attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, block_siz
         if causal:
             n = end - start
             scores = np.where(np.triu(np.ones((n, n), dtype=bool), 1), -np.inf, scores)
+        if mask is not None:
+            part = np.asarray(mask)[..., start:end, start:end]
+            if part.dtype == np.bool_:
+                scores = np.where(part, scores, -np.inf)
+            else:
+                scores = scores + part.astype(np.float64)
         p, _ = softmax_lse(scores)
+        dead = np.all(np.isneginf(scores), axis=-1, keepdims=True)
+        p = np.where(dead, np.nan, p)
         out[..., start:end, :] = np.matmul(p, v64[..., start:end, :])
     return round_dtype(out, out_dtype)
 

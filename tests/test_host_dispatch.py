@@ -98,7 +98,7 @@ class DummyModel:
 @pytest.mark.parametrize("kwargs,reason", [
     (dict(), "not_cuda"),
     (dict(block_size=32), "unsupported_block_size_32"),
-    (dict(mask=torch.zeros(64, 64)), "arbitrary_mask"),
+    (dict(mask=torch.zeros(64, 64)), "not_cuda"),     # masks run on the kernel; CPU tensors do not
 ])
 def test_dispatch_fallback_reasons(kwargs, reason):
     q = torch.randn(1, 1, 64, 32, dtype=torch.float16)
@@ -179,3 +179,54 @@ def test_full_attention_validation_reasons():
     assert validate_full_attention_triton_bh(q[..., :96], k[..., :96], k[..., :96])["reason"] == "unsupported_head_dim_96"
     with pytest.raises(ValueError, match="unavailable: not_cuda"):
         full_attention_hip(q, k, torch.randn_like(k))
+
+
+@pytest.mark.parametrize("layout,shape,mask_shape", [
+    ("bhtd", (2, 3, 130, 32), (130, 130)),
+    ("bhtd", (2, 3, 130, 32), (2, 130, 130)),        # per batch, repeated over heads
+    ("bhtd", (2, 3, 130, 32), (1, 130, 130)),
+    ("bhtd", (2, 3, 130, 32), (6, 130, 130)),        # per (batch, head)
+    ("bhtd", (2, 3, 130, 32), (2, 3, 130, 130)),
+    ("bhtd", (2, 3, 130, 32), (1, 3, 130, 130)),
+    ("bhtd", (2, 3, 130, 32), (2, 1, 130, 130)),
+    ("bh_t_d", (6, 130, 32), (6, 130, 130)),
+    ("bh_t_d", (6, 130, 32), (1, 130, 130)),
+])
+@pytest.mark.parametrize("dtype", [torch.bool, torch.float32, torch.float64])
+def test_kernel_mask_view_matches_eager_slices(layout, shape, mask_shape, dtype):
+    """The [B',H',T,T] view the kernel reads equals the eager loop's per-block slices (reference.py:114-156)."""
+    from rdna35_block_attention.reference import _mask_block, mask_view_bhtt, normalize_qkv_to_bh_t_d
+
+    q = torch.randn(shape)
+    q_flat, _, _, info = normalize_qkv_to_bh_t_d(q, q, q, layout=layout)
+    bh = q_flat.shape[0]
+    gen = torch.Generator().manual_seed(sum(mask_shape))
+    raw = torch.rand(mask_shape, generator=gen)
+    mask = raw < 0.5 if dtype == torch.bool else raw.to(dtype)
+    view = mask_view_bhtt(mask, batch_heads=bh, info=info, device=q.device)
+    assert view.ndim == 4 and view.shape[0] * view.shape[1] == bh
+    assert view.dtype == (torch.bool if dtype == torch.bool else torch.float32)
+    flat = view.reshape(bh, info.tokens, info.tokens)
+    for start in range(0, info.tokens, 64):
+        end = min(start + 64, info.tokens)
+        eager = _mask_block(mask, start, end, batch_heads=bh, info=info, device=q.device)
+        torch.testing.assert_close(flat[:, start:end, start:end], eager.to(flat.dtype))
+
+
+def test_kernel_mask_view_errors_match_eager():
+    from rdna35_block_attention.reference import _mask_block, mask_view_bhtt, normalize_qkv_to_bh_t_d
+
+    q = torch.randn(2, 3, 130, 32)
+    _, _, _, info = normalize_qkv_to_bh_t_d(q, q, q, layout="bhtd")
+    bad = [torch.zeros(130, 129), torch.zeros(4, 130, 130), torch.zeros(3, 3, 130, 130), torch.zeros(2, 2, 130, 130),
+           torch.zeros(2, 3, 130, 130, 1)]
+    for mask in bad:
+        with pytest.raises(ValueError) as eager:
+            _mask_block(mask, 0, 64, batch_heads=6, info=info, device=q.device)
+        with pytest.raises(ValueError) as kernel:
+            mask_view_bhtt(mask, batch_heads=6, info=info, device=q.device)
+        assert str(kernel.value) == str(eager.value)
+    q3 = torch.randn(6, 130, 32)
+    _, _, _, info3 = normalize_qkv_to_bh_t_d(q3, q3, q3, layout="bh_t_d")
+    with pytest.raises(ValueError, match="4D mask requires"):
+        mask_view_bhtt(torch.zeros(1, 1, 130, 130), batch_heads=6, info=info3, device=q.device)

@@ -102,6 +102,49 @@ def test_fixed_block_equals_masked_dense_softmax(tokens, causal):
     np.testing.assert_allclose(oatt.fixed_block_attention(q, k, v, causal=causal), expected, rtol=1e-5, atol=1e-6)
 
 
+def test_fixed_block_mask_pins():
+    """Masked block loop (reference.py:186-195) against identities that do not restate it."""
+    rng = np.random.default_rng(11)
+    tokens = 150
+    q, k, v = (rng.standard_normal((3, tokens, 32)) for _ in range(3))
+    plain = oatt.fixed_block_attention(q, k, v)
+    # all-true bool mask and zero additive mask change nothing
+    np.testing.assert_array_equal(oatt.fixed_block_attention(q, k, v, mask=np.ones((tokens, tokens), bool)), plain)
+    np.testing.assert_array_equal(oatt.fixed_block_attention(q, k, v, mask=np.zeros((tokens, tokens))), plain)
+    # a lower-triangular bool mask is causal attention
+    tril = np.tril(np.ones((tokens, tokens), bool))
+    np.testing.assert_allclose(oatt.fixed_block_attention(q, k, v, mask=tril),
+                               oatt.fixed_block_attention(q, k, v, causal=True), rtol=0, atol=0)
+    # softmax is shift invariant per row: a per-row constant additive mask changes nothing
+    shift = np.broadcast_to(rng.standard_normal((tokens, 1)) * 5, (tokens, tokens))
+    np.testing.assert_allclose(oatt.fixed_block_attention(q, k, v, mask=shift), plain, rtol=1e-9, atol=1e-12)
+    # -inf additive entries are the same as false bool entries
+    keep = rng.random((3, tokens, tokens)) < 0.6
+    np.fill_diagonal(keep[0], True)
+    keep[1:] |= np.eye(tokens, dtype=bool)
+    additive = np.where(keep, 0.0, -np.inf)
+    np.testing.assert_array_equal(oatt.fixed_block_attention(q, k, v, mask=additive),
+                                  oatt.fixed_block_attention(q, k, v, mask=keep))
+    # one kept key per row returns that key's value row exactly
+    one = np.zeros((tokens, tokens), bool)
+    target = np.array([(i // 64) * 64 + (i * 7) % min(64, tokens - (i // 64) * 64) for i in range(tokens)])
+    one[np.arange(tokens), target] = True
+    np.testing.assert_array_equal(oatt.fixed_block_attention(q, k, v, mask=one), v[:, target, :].astype(np.float32))
+    # a row with nothing kept is NaN (torch.softmax of an all -inf row), other rows unaffected
+    hole = np.ones((tokens, tokens), bool)
+    hole[5, :] = False
+    out = oatt.fixed_block_attention(q, k, v, mask=hole)
+    assert np.isnan(out[:, 5]).all()
+    np.testing.assert_array_equal(np.delete(out, 5, axis=1), np.delete(plain, 5, axis=1))
+    # torch restatement: SDPA with (block mask AND user mask)
+    user = rng.random((tokens, tokens)) < 0.7
+    user |= np.eye(tokens, dtype=bool)
+    combined = oatt.block_diagonal_mask(tokens, 64) & user
+    expected = F.scaled_dot_product_attention(*(torch.from_numpy(x) for x in (q, k, v)),
+                                              attn_mask=torch.from_numpy(combined)).numpy()
+    np.testing.assert_allclose(oatt.fixed_block_attention(q, k, v, mask=user), expected, rtol=1e-5, atol=1e-6)
+
+
 # ----------------------------------------------------------------------------- statistics
 def test_hyd_stats_textbook():
     q, k, v = (_rng_bf16((2, 200, D), s) for s in (3, 4, 5))
