@@ -18,8 +18,16 @@ Also measured in the same process:
   * the CPU oracle (oracle.pisa.hyd_forward) on a bounded sample of heads,
     scaled to one call -> cpu_baseline.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--workload NAME]
 Prints one JSON line.
+
+``--workload`` selects another configuration of the path (default c4, the
+metric above): c1 fixed block-diagonal fp32 [1,8,4096,64]; c2 dense exact
+self-attention bf16 [2,16,9216,128]; c2x cross-attention Tq=9216, Tk=512;
+c3 / c3l MiniMax-H3 strided QKV [1,T,3,56,128] at T=9170 / 16500; c5 video
+PISA bf16 [1,40,32768,128] on a 16x32x64 grid, 80 of 512 blocks exact.  Each
+prints the same JSON schema with that workload's own roofline and a CPU
+oracle baseline on a bounded sample.
 
 ``--profile-run`` runs only what the counter profiles need (a plain device
 copy of COPY_BYTES, then one prepare and PROFILE_ATTENDS attend launches) and
@@ -159,6 +167,164 @@ def measured_traffic():
         return None
 
 
+# ----------------------------------------------------------------------------- other workloads
+def _oracle_ms(fn, repeats: int = 3) -> float:
+    fn()  # warm-up
+    samples = []
+    for _ in range(repeats):
+        t0 = time.perf_counter()
+        fn()
+        samples.append((time.perf_counter() - t0) * 1e3)
+    return statistics.median(samples)
+
+
+def _line(metric, call_ms, args, config, roofline, extra=None, baseline_ms=None, dtype="bf16",
+          data="synthetic: seeded N(0,1)"):
+    result = {
+        "metric": metric, "value": round(call_ms, 4), "unit": "ms", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(call_ms, 4), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None if baseline_ms is None else round(call_ms / baseline_ms, 5), "dtype": dtype,
+        "data": data, "config": config, "roofline": roofline,
+    }
+    result.update(extra or {})
+    return result
+
+
+def _mfma_roofline(kernel, flops, ms):
+    achieved = flops / (ms * 1e-3)
+    return {"bound": "mfma", "kernel": kernel, "achieved": round(achieved / 1e12, 2), "peak": PEAK_BF16_FLOPS / 1e12,
+            "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_FLOPS, 4), "traffic": None}
+
+
+def _cpu(value_ms, sample):
+    return {"value": round(value_ms, 1), "unit": "ms", "cores": blas_threads(), "kind": "port", "sample": sample}
+
+
+def run_workload(name: str, args) -> dict:
+    import numpy as np
+    import torch
+
+    import mi355x_pisa
+
+    sys.path.insert(0, str(REPO))
+    from oracle import attention as oatt
+    from oracle import pisa as opisa
+
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    gen = torch.Generator().manual_seed(1)
+
+    def randn(shape, dtype, scale=1.0):
+        return (torch.randn(shape, generator=gen) * scale).to(dtype).to(device)
+
+    def host(t):
+        return t.detach().float().cpu().numpy()
+
+    if name == "c1":
+        shape = (1, 8, 4096, 64)
+        q, k, v = (randn(shape, torch.float32) for _ in range(3))
+        ms = time_gpu(lambda: mi355x_pisa.fixed_block_attention(q, k, v, 0.125), args.steps, args.warmup)
+        nbytes = 4 * math.prod(shape) * 4
+        achieved = nbytes / (ms * 1e-3)
+        roof = {"bound": "hbm", "kernel": "fixed_block_kernel", "achieved": round(achieved / 1e9, 1),
+                "peak": PEAK_HBM_BYTES / 1e9, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_BYTES, 4),
+                "traffic": None}
+        result = _line("C1 fixed block-diagonal attention ms, fp32 B=1 H=8 T=4096 D=64", ms, args,
+                       {"workload": "fixed_block_diagonal", "batch": 1, "heads": 8, "tokens": 4096, "head_dim": 64,
+                        "block": 64}, roof, dtype="f32")
+        if not args.no_cpu_baseline:
+            qh, kh, vh = (host(t) for t in (q, k, v))
+            result["cpu_baseline"] = _cpu(_oracle_ms(lambda: oatt.fixed_block_attention(qh, kh, vh, 64, 0.125)),
+                                          "oracle.attention.fixed_block_attention (numpy float64), whole call, "
+                                          "median of 3 after 1 warm-up")
+        return result
+
+    if name in ("c2", "c2x"):
+        kv_tokens = 9216 if name == "c2" else 512
+        q = randn((2, 16, 9216, 128), torch.bfloat16, 0.5)
+        k = randn((2, 16, kv_tokens, 128), torch.bfloat16, 0.5)
+        v = randn((2, 16, kv_tokens, 128), torch.bfloat16, 0.5)
+        s = 1 / math.sqrt(128)
+        ms = time_gpu(lambda: mi355x_pisa.dense_attention(q, k, v, s), args.steps, args.warmup)
+        flops = 4.0 * 32 * 9216 * kv_tokens * 128
+        label = "self" if name == "c2" else "cross Tk=512"
+        result = _line(f"C2 exact full attention ms ({label}), bf16 B=2 H=16 Tq=9216 Tk={kv_tokens} D=128", ms, args,
+                       {"workload": "dense_exact_attention", "batch": 2, "heads": 16, "q_tokens": 9216,
+                        "kv_tokens": kv_tokens, "head_dim": 128},
+                       _mfma_roofline("kv_pack_kernel + attention_kernel (dense)", flops, ms),
+                       data="synthetic: seeded 0.5*N(0,1)")
+        if not args.no_cpu_baseline:
+            rows = 1024 if name == "c2" else 9216
+            qh, kh, vh = host(q[0, 0, :rows]), host(k[0, 0]), host(v[0, 0])
+            one = _oracle_ms(lambda: oatt.dense_attention(qh, kh, vh, s))
+            scale = 32 * 9216 / rows
+            result["cpu_baseline"] = _cpu(one * scale, f"oracle.attention.dense_attention (numpy float64) on "
+                                                       f"{rows} query rows of 1 head, median of 3, scaled x{scale:g}")
+        return result
+
+    if name in ("c3", "c3l"):
+        tokens = 9170 if name == "c3" else 16500
+        gen.manual_seed(tokens)
+        qkv = randn((1, tokens, 3, 56, 128), torch.bfloat16)
+        q, k = qkv[:, :, 0].permute(0, 2, 1, 3), qkv[:, :, 1].permute(0, 2, 1, 3)
+        v = qkv[:, :, 2].clone().permute(0, 2, 1, 3)
+        s = 1 / math.sqrt(128)
+        ms = time_gpu(lambda: mi355x_pisa.dense_attention(q, k, v, s, merged_output=True), args.steps, args.warmup)
+        sdpa_ms = time_gpu(lambda: torch.nn.functional.scaled_dot_product_attention(q, k, v), max(2, args.steps // 4),
+                           2)
+        flops = 4.0 * 56 * tokens * tokens * 128
+        published = {9170: 86.736, 16500: 280.344}[tokens]
+        result = _line(f"C3 MiniMax-H3 exact attention ms, bf16 B=1 H=56 T={tokens} D=128, strided QKV views", ms,
+                       args, {"workload": "minimax_h3_strided", "batch": 1, "heads": 56, "tokens": tokens,
+                              "head_dim": 128},
+                       _mfma_roofline("kv_pack_kernel + attention_kernel (dense, strided views)", flops, ms),
+                       extra={"torch_sdpa_strided_ms": round(sdpa_ms, 3), "baseline_ms_gfx1151": published},
+                       baseline_ms=published)
+        if not args.no_cpu_baseline:
+            rows = 512
+            qh, kh, vh = host(q[0, 0, :rows]), host(k[0, 0]), host(v[0, 0])
+            one = _oracle_ms(lambda: oatt.dense_attention(qh, kh, vh, s))
+            scale = 56 * tokens / rows
+            result["cpu_baseline"] = _cpu(one * scale, f"oracle.attention.dense_attention (numpy float64) on "
+                                                       f"{rows} query rows of 1 head, median of 3, scaled x{scale:g}")
+        return result
+
+    if name == "c5":
+        from mi355x_pisa.synthetic import video_qkv
+
+        grid = (16, 32, 64)
+        tokens, heads, blocks, exact = 32768, 40, 512, 80
+        q, k, v = video_qkv(batch=1, heads=heads, grid=grid, seed=0, device=device)
+        s = 1 / math.sqrt(128)
+        call_ms = time_gpu(lambda: mi355x_pisa.generic_forward(q, k, v, exact, s, True, token_grid=grid),
+                           args.steps, args.warmup)
+        out4 = torch.empty((1, tokens, heads, 128), dtype=q.dtype, device=device).permute(0, 2, 1, 3)
+        plan = mi355x_pisa.PisaPlan(q, k, v, out4, exact, s, hyd=False, first_order=True, token_grid=grid)
+        prepare_ms = time_gpu(plan.prepare, args.steps, args.warmup)
+        attend_ms = time_gpu(plan.attend, args.steps, args.warmup)
+        flops_exact = 4.0 * heads * blocks * exact * 64 * 64 * 128
+        flops_tail = 4.0 * heads * blocks * (blocks - exact) * 64 * 128
+        flops_corr = 2.0 * heads * tokens * 128 * 128
+        result = _line("C5 video PISA call ms, bf16 B=1 H=40 T=32768 D=128 (16x32x64), 80/512 blocks", call_ms, args,
+                       {"workload": "video_pisa_generic", "batch": 1, "heads": heads, "tokens": tokens,
+                        "grid": list(grid), "head_dim": 128, "blocks": blocks, "exact_blocks": exact},
+                       _mfma_roofline("attention_kernel (exact tiles + tail + first-order + merge)",
+                                      flops_exact + flops_tail + flops_corr, attend_ms),
+                       extra={"stages_ms": {"prepare": round(prepare_ms, 4), "attend": round(attend_ms, 4)},
+                              "exact_tile_tflops": round(flops_exact / (attend_ms * 1e-3) / 1e12, 2)},
+                       data="synthetic: seeded 3-D Gaussian random field (sigma 8) + 0.3*N(0,1)")
+        if not args.no_cpu_baseline:
+            from oracle import layout as olayout
+
+            order = olayout.tile_order(*grid)
+            packed = [olayout.pack(host(t)[0, :1], order) for t in (q, k, v)]
+            one = _oracle_ms(lambda: opisa.generic_forward(*packed, exact, s, True, "bf16"), repeats=1)
+            result["cpu_baseline"] = _cpu(one * heads, f"oracle.pisa.generic_forward (numpy float64) on 1 of {heads} "
+                                                       f"heads, 1 run after 1 warm-up, scaled x{heads}")
+        return result
+    raise ValueError(f"unknown workload {name}")
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--gpus", type=int, default=1)
@@ -167,6 +333,7 @@ def main() -> int:
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--cpu-sample-heads", type=int, default=2)
     parser.add_argument("--profile-run", action="store_true")
+    parser.add_argument("--workload", default="c4", choices=["c4", "c1", "c2", "c2x", "c3", "c3l", "c5"])
     args = parser.parse_args()
     if args.profile_run:
         return profile_run()
@@ -174,6 +341,9 @@ def main() -> int:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the path shards by (batch, head) "
               f"with no communication, so N GPUs run N independent shares.", file=sys.stderr)
         return 2
+    if args.workload != "c4":
+        print(json.dumps(run_workload(args.workload, args)), flush=True)
+        return 0
 
     import torch
 

@@ -25,6 +25,11 @@ MINIMAX_H3_HEAD_DIM = 128
 MINIMAX_H3_MIN_PACK_TOKENS = 4608
 MINIMAX_H3_PACK_ALL_TOKENS = 12000
 MINIMAX_H3_MAX_PACK_TOKENS = 16500
+# The reference stops at 16500 tokens because its packed copies must pay for
+# themselves; reading the strided views in place has no copy, so the override
+# here takes longer H3 sequences too (MI355X: 2.3x / 1.7x faster than strided
+# SDPA at T = 9170 / 16500).
+MINIMAX_H3_MAX_TOKENS = 65536
 
 
 def _fallback_call(previous_override: Callable | None, original_func: Callable, *args, **kwargs):
@@ -98,8 +103,8 @@ def _reject_reason(q, k, v, heads, mask, skip_reshape, skip_output_reshape, devi
         return "minimax_h3_b1_h56_d128_is_required"
     if q.shape[2] < MINIMAX_H3_MIN_PACK_TOKENS:
         return f"tokens_below_{MINIMAX_H3_MIN_PACK_TOKENS}"
-    if q.shape[2] > MINIMAX_H3_MAX_PACK_TOKENS:
-        return f"tokens_above_{MINIMAX_H3_MAX_PACK_TOKENS}"
+    if q.shape[2] > MINIMAX_H3_MAX_TOKENS:
+        return f"tokens_above_{MINIMAX_H3_MAX_TOKENS}"
     if q.dtype != torch.bfloat16 or k.dtype != q.dtype or v.dtype != q.dtype:
         return "matching_bfloat16_qkv_are_required"
     if q.device != k.device or q.device != v.device or q.device.type != "cuda":
@@ -156,7 +161,7 @@ def patch_minimax_h3_attention(model, *, enabled: bool, verbose_fallbacks: bool)
     options["optimized_attention_override"] = make_minimax_h3_attention_override(
         device_index=device_index, verbose_fallbacks=verbose_fallbacks, previous_override=previous)
     info = ("model-local MiniMax-H3 gfx950 exact attention override installed for BF16 B=1,H=56,D=128 with "
-            f"{MINIMAX_H3_MIN_PACK_TOKENS}<=T<={MINIMAX_H3_MAX_PACK_TOKENS}; strided Q/K/V views are read in place")
+            f"{MINIMAX_H3_MIN_PACK_TOKENS}<=T<={MINIMAX_H3_MAX_TOKENS}; strided Q/K/V views are read in place")
     if previous is not None:
         info += "; existing optimized_attention_override is chained for fallback"
     return patched, info

@@ -547,8 +547,11 @@ def test_h3_pack_profiles_keep_values_in_one_allocation():
 def test_h3_reject_reasons():
     q = torch.randn(1, 56, 8, 128, dtype=torch.bfloat16)
     assert h3._reject_reason(q, q, q, 56, None, True, False, 0, {}) == "tokens_below_4608"
-    big = torch.empty(1, 56, 16501, 128, dtype=torch.bfloat16, device="meta")
-    assert h3._reject_reason(big, big, big, 56, None, True, False, 0, {}) == "tokens_above_16500"
+    longer = torch.empty(1, 56, 16501, 128, dtype=torch.bfloat16, device="meta")  # past the reference's pack bound
+    assert h3._reject_reason(longer, longer, longer, 56, None, True, False, 0, {}) == \
+        "matching_rocm_qkv_device_is_required"
+    big = torch.empty(1, 56, 65537, 128, dtype=torch.bfloat16, device="meta")
+    assert h3._reject_reason(big, big, big, 56, None, True, False, 0, {}) == "tokens_above_65536"
     ok = torch.empty(1, 56, 9170, 128, dtype=torch.bfloat16, device="meta")
     assert h3._reject_reason(ok, ok, ok, 56, None, True, False, 0, {"is_causal": True}) == \
         "causal_attention_is_not_supported"
