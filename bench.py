@@ -25,9 +25,11 @@ Prints one JSON line.
 metric above): c1 fixed block-diagonal fp32 [1,8,4096,64]; c2 dense exact
 self-attention bf16 [2,16,9216,128]; c2x cross-attention Tq=9216, Tk=512;
 c3 / c3l MiniMax-H3 strided QKV [1,T,3,56,128] at T=9170 / 16500; c5 video
-PISA bf16 [1,40,32768,128] on a 16x32x64 grid, 80 of 512 blocks exact.  Each
-prints the same JSON schema with that workload's own roofline and a CPU
-oracle baseline on a bounded sample.
+PISA bf16 [1,40,32768,128] on a 16x32x64 grid, 80 of 512 blocks exact; pack
+/ unpack / epilogue the standalone C4 layout kernels of the reference's
+native API (raster -> 8x8-tile pack of Q/K/V, its inverse, the fused LSE
+merge epilogue).  Each prints the same JSON schema with that workload's own
+roofline and a CPU oracle baseline on a bounded sample.
 
 ``--profile-run`` runs only what the counter profiles need (a plain device
 copy of COPY_BYTES, then one prepare and PROFILE_ATTENDS attend launches) and
@@ -322,6 +324,58 @@ def run_workload(name: str, args) -> dict:
             result["cpu_baseline"] = _cpu(one * heads, f"oracle.pisa.generic_forward (numpy float64) on 1 of {heads} "
                                                        f"heads, 1 run after 1 warm-up, scaled x{heads}")
         return result
+    if name in ("pack", "unpack", "epilogue"):
+        from oracle import layout as olayout
+
+        native = mi355x_pisa._C
+        shape = (BATCH, HEADS, TOKENS, HEAD_DIM)
+        storage = [randn((BATCH, TOKENS, HEADS, HEAD_DIM), torch.bfloat16) for _ in range(3)]
+        q, k, v = (t.permute(0, 2, 1, 3) for t in storage)  # the Anima BHTD views
+        elem = BATCH * HEADS * TOKENS * HEAD_DIM
+        bh = BATCH * HEADS
+        order = olayout.tile_order(1, SIDE, SIDE)
+        if name == "pack":
+            fn = lambda: native.pack_spatial_qkv(q, k, v)
+            nbytes = 6 * elem * 2  # read and write Q, K, V
+            kernel = "pack_kernel"
+            host_q = host(q).reshape(bh, TOKENS, HEAD_DIM)
+            cpu_fn = lambda: [olayout.pack(x, order) for x in (host_q, host_q, host_q)]
+            cpu_note = "oracle.layout.pack (numpy take) of Q, K, V"
+        elif name == "unpack":
+            packed = randn((bh, TOKENS, HEAD_DIM), torch.bfloat16)
+            fn = lambda: native.unpack_spatial_output(packed, BATCH, HEADS)
+            nbytes = 2 * elem * 2
+            kernel = "unpack_kernel"
+            host_p = host(packed)
+            cpu_fn = lambda: olayout.unpack(host_p, order)
+            cpu_note = "oracle.layout.unpack (numpy) of the output"
+        else:
+            exact_o = randn((bh, TOKENS, HEAD_DIM), torch.bfloat16)
+            approx_o = randn((bh, TOKENS, HEAD_DIM), torch.bfloat16)
+            exact_l = randn((bh, TOKENS), torch.float32)
+            approx_l = randn((bh, TOKENS), torch.float32)
+            corr = randn((bh, TOKENS, HEAD_DIM), torch.float32)
+            fn = lambda: native.fuse_spatial_epilogue(exact_o, exact_l, approx_o, approx_l, corr, BATCH, HEADS)
+            nbytes = elem * 2 * 3 + elem * 4 + bh * TOKENS * 4 * 2  # 2 bf16 reads + fp32 correction + out + LSEs
+            kernel = "merge_kernel"
+            eo, ao, el, al, co = (host(t) for t in (exact_o, approx_o, exact_l, approx_l, corr))
+
+            def cpu_fn():
+                m = np.maximum(el, al)
+                lse = m + np.log(np.exp(el - m) + np.exp(al - m))
+                merged = eo * np.exp(el - lse)[..., None] + (ao + co) * np.exp(al - lse)[..., None]
+                return olayout.unpack(merged, order)
+            cpu_note = "numpy LSE merge + unpack (the fused_spatial_epilogue formula)"
+        ms = time_gpu(fn, args.steps, args.warmup)
+        achieved = nbytes / (ms * 1e-3)
+        roof = {"bound": "hbm", "kernel": kernel, "achieved": round(achieved / 1e9, 1), "peak": PEAK_HBM_BYTES / 1e9,
+                "unit": "GB/s", "frac": round(achieved / PEAK_HBM_BYTES, 4), "traffic": None}
+        result = _line(f"C4 standalone {name} ms, bf16 B=2 H=16 T=9216 D=128 ({nbytes / 1e6:.1f} MB)", ms, args,
+                       {"workload": f"spatial_{name}", "batch": BATCH, "heads": HEADS, "tokens": TOKENS,
+                        "head_dim": HEAD_DIM}, roof, extra={"algorithmic_bytes": nbytes})
+        if not args.no_cpu_baseline:
+            result["cpu_baseline"] = _cpu(_oracle_ms(cpu_fn), f"{cpu_note}, whole call, median of 3 after 1 warm-up")
+        return result
     raise ValueError(f"unknown workload {name}")
 
 
@@ -333,7 +387,8 @@ def main() -> int:
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--cpu-sample-heads", type=int, default=2)
     parser.add_argument("--profile-run", action="store_true")
-    parser.add_argument("--workload", default="c4", choices=["c4", "c1", "c2", "c2x", "c3", "c3l", "c5"])
+    parser.add_argument("--workload", default="c4",
+                        choices=["c4", "c1", "c2", "c2x", "c3", "c3l", "c5", "pack", "unpack", "epilogue"])
     args = parser.parse_args()
     if args.profile_run:
         return profile_run()
