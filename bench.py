@@ -19,7 +19,10 @@ Also measured in the same process:
     scaled to one call -> cpu_baseline.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--workload NAME]
-Prints one JSON line.
+Prints one JSON line.  Defaults: 200 timed steps after 100 untimed warm-up
+steps per timed region.  The GPU's clocks settle only after some tens of
+milliseconds of back-to-back launches (the attention kernel runs ~6 % slower
+over the first ~20 launches after idle), so short warm-ups time the ramp.
 
 ``--workload`` selects another configuration of the path (default c4, the
 metric above): c1 fixed block-diagonal fp32 [1,8,4096,64]; c2 dense exact
@@ -382,8 +385,8 @@ def run_workload(name: str, args) -> dict:
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--gpus", type=int, default=1)
-    parser.add_argument("--steps", type=int, default=20)
-    parser.add_argument("--warmup", type=int, default=5)
+    parser.add_argument("--steps", type=int, default=200)
+    parser.add_argument("--warmup", type=int, default=100)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--cpu-sample-heads", type=int, default=2)
     parser.add_argument("--profile-run", action="store_true")
