@@ -53,31 +53,41 @@ __device__ __forceinline__ float sum8(f16x8 x, float acc) {
     return __builtin_amdgcn_fdot2(__builtin_shufflevector(x, x, 6, 7), one, acc, false);
 }
 
-// The chunk loop works on 32-key half chunks.  For half h the running max is
-// updated first (a short branchy step), then one straight-line region issues
-// the 16 score MFMAs of half h+1 interleaved with the exponentials of half h,
-// and the 16 PV MFMAs of half h interleaved with the operand loads of the
-// next chunk, so that VALU, memory and MFMA work of one wave overlap.
+// The chunk loop works on 32-key half chunks.  One straight-line region per
+// half h issues the 16 score MFMAs of half h+1 interleaved with the
+// exponentials of half h, then the 16 PV MFMAs of half h interleaved with the
+// operand loads of the next chunk and with the masking and column maxima of
+// half h+1 (whose scores are ready by then); only the rare running-max move
+// branches, after the region.  VALU, memory and MFMA work of the one wave on
+// the SIMD thus overlap.
 
-// Running-max update for half-chunk scores s[nt] (s[nt][v] = raw score of key
-// 8(v/4) + 4half + v%4 of the half, query tile nt, column col); `c` converts
-// raw scores to log2 units.  The running max only moves when a column's max
-// exceeds it by kLazyRescale, so the O rescale runs on the first half chunk
-// and rarely after; probabilities stay below 2^kLazyRescale.
-template <int NT, int MD>
-__device__ __forceinline__ void rescale_half(const f32x16 (&s)[NT], float c, float (&m)[NT], float (&l)[NT],
-                                             float (&lt)[NT], f32x16 (&o)[MD][NT]) {
-    float mx[NT];
-    bool need[NT];
-    bool any_need = false;
+// Column maxima of half-chunk scores s[nt] (s[nt][v] = score of key
+// 8(v/4) + 4half + v%4 of the half, query tile nt, column col) in log2 units
+// (`c` converts the scores to them).
+template <int NT>
+__device__ __forceinline__ void half_max(const f32x16 (&s)[NT], float c, float (&mx)[NT]) {
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
         float x = s[nt][0];
 #pragma unroll
         for (int v = 1; v < 16; ++v) x = fmaxf(x, s[nt][v]);
-        x = max_xor32(x);
-        mx[nt] = x * c;
-        need[nt] = mx[nt] > m[nt] + kLazyRescale;
+        mx[nt] = max_xor32(x) * c;
+    }
+}
+
+// Running-max update from the column maxima mx of the next half.  The running
+// max only moves when a column's max exceeds it by kLazyRescale, so the O
+// rescale runs on the first half chunk and rarely after; probabilities stay
+// below 2^kLazyRescale.  `enable` false (scores past the last chunk) leaves
+// the state unchanged.
+template <int NT, int MD>
+__device__ __forceinline__ void rescale_to(const float (&mx)[NT], bool enable, float (&m)[NT], float (&l)[NT],
+                                          float (&lt)[NT], f32x16 (&o)[MD][NT]) {
+    bool need[NT];
+    bool any_need = false;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        need[nt] = enable && mx[nt] > m[nt] + kLazyRescale;
         any_need = any_need || need[nt];
     }
     if (__any(any_need)) {
@@ -257,6 +267,9 @@ void attention_kernel(AttnArgs a, const int32_t* __restrict__ sel, const uint32_
 #pragma unroll
                 for (int nt = 0; nt < NT; ++nt) o[md][nt] = mfma32(vf[md][2 * mt + ss], pf[nt][ss], o[md][nt]);
     };
+    // Whether half chunks of chunk x (table row `row`) need transform_half: tail
+    // chunks and a short last key block (wave-uniform).
+    auto special = [&](int x, int row) { return is_tail(x) || (row + 1) * kBlock > a.kv_tokens; };
     // Masks / tail bias of half mt of chunk x (row = its table row); returns
     // the factor that converts the resulting scores to log2 units.
     auto transform_half = [&](int x, int row, int mt, f32x16 (&s)[NT]) -> float {
@@ -287,50 +300,71 @@ void attention_kernel(AttnArgs a, const int32_t* __restrict__ sel, const uint32_
         return 1.0f;
     };
 
+    // Column maxima of half mt of chunk x, then the running-max update.  The
+    // common half (exact, full block) takes no branch before its maxima, so
+    // they are computed in the region of the preceding PV MFMAs; tail chunks
+    // and a short last block are transformed and re-maxed on a side path.
+    auto check_half = [&](int x, int row, int mt, f32x16 (&s)[NT], bool enable) -> float {
+        float mx[NT];
+        half_max<NT>(s, c, mx);
+        float f = c;
+        if (special(x, row)) {
+            f = transform_half(x, row, mt, s);
+            half_max<NT>(s, f, mx);
+        }
+        rescale_to<NT, MD>(mx, enable, m, l, lt, o);
+        return f;
+    };
+
     f32x16 sa[NT], sb[NT];  // scores of the first / second half of the current chunk
+    float ca = c;           // factor to log2 units of the (transformed) scores in sa
     int row0 = 0, row1 = 0;
     if (n_chunks > 0) {
         row0 = table_row(0);
         row1 = table_row(1);
         const char* k0 = kptr(0, row0);
         const char* v0 = vptr(0, row0);
+        // The loop sits inside this block: entered only after the query loads
+        // have landed (the first scores use them), the compiler's wait counts
+        // at the loop head cover just the chunk loads in flight.  The loads
+        // after the first scores go out in the loop's order (K half 1, V half
+        // 0, next K half 0, V half 1).
         load_k_half(kf[0], k0, 0);
         load_k_half(kf[1], k0, 1);
         load_v_half(v0, 0);
-        load_v_half(v0, 1);
         pin_q();
         scores_half(kf[0], sa);
         load_k_half(kf[0], kptr(1, row1), 0);
-    }
-    for (int cc = 0; cc < n_chunks; ++cc) {
-        pin_q();
-        const int row2 = table_row(cc + 2);
-        const bool tail = is_tail(cc);
-        const bool last = cc + 1 == n_chunks;
-        const char* kn = (first_order && last) ? ht : kptr(cc + 1, row1);
-        const char* vn = (first_order && last) ? ht + 16 * 1024 : vptr(cc + 1, row1);
-        const char* kn2 = (first_order && last) ? ht : kptr(cc + 2, row2);
-        vec8 pf[NT][2];
+        load_v_half(v0, 1);
+        ca = check_half(0, row0, 0, sa, true);
+        for (int cc = 0; cc < n_chunks; ++cc) {
+            const int row2 = table_row(cc + 2);
+            const bool tail = is_tail(cc);
+            const bool last = cc + 1 == n_chunks;
+            const char* kn = (first_order && last) ? ht : kptr(cc + 1, row1);
+            const char* vn = (first_order && last) ? ht + 16 * 1024 : vptr(cc + 1, row1);
+            const char* kn2 = (first_order && last) ? ht : kptr(cc + 2, row2);
+            vec8 pf[NT][2];
 
-        // ---- first half: scores in sa (issued one half earlier)
-        const float ca = transform_half(cc, row0, 0, sa);
-        rescale_half<NT, MD>(sa, ca, m, l, lt, o);
-        scores_half(kf[1], sb);
-        probs_half<T, NT>(sa, ca, m, l, lt, tail, pf);
-        load_k_half(kf[1], kn, 1);
-        pv_half(0, pf);
-        load_v_half(vn, 0);
+            // ---- first half: scores in sa (issued, masked and max-checked one half earlier)
+            scores_half(kf[1], sb);
+            probs_half<T, NT>(sa, ca, m, l, lt, tail, pf);
+            load_k_half(kf[1], kn, 1);
+            pv_half(0, pf);
+            load_v_half(vn, 0);
+            const float cb = check_half(cc, row0, 1, sb, true);
 
-        // ---- second half: scores in sb; also scores the next chunk's first half
-        const float cb = transform_half(cc, row0, 1, sb);
-        rescale_half<NT, MD>(sb, cb, m, l, lt, o);
-        scores_half(kf[0], sa);
-        probs_half<T, NT>(sb, cb, m, l, lt, tail, pf);
-        load_k_half(kf[0], kn2, 0);
-        pv_half(1, pf);
-        load_v_half(vn, 1);
-        row0 = row1;
-        row1 = row2;
+            // ---- second half: scores in sb; also scores the next chunk's first half
+            // (past the end on the last iteration: computed, never used)
+            scores_half(kf[0], sa);
+            probs_half<T, NT>(sb, cb, m, l, lt, tail, pf);
+            load_k_half(kf[0], kn2, 0);
+            pv_half(1, pf);
+            load_v_half(vn, 1);
+            ca = check_half(cc + 1, row1, 0, sa, !last);
+            row0 = row1;
+            row1 = row2;
+        }
     }
 
     // ---- epilogue: normalise, add the first-order correction one 32-dim
