@@ -289,7 +289,8 @@ static int validate_forward(int32_t dtype, int32_t batch, int32_t heads, int32_t
 
 static int route_impl(const ForwardBuffers& w, int32_t head_dim, int32_t exact_blocks, float scale,
                       int32_t sink_block, int32_t route_mode, int32_t* debug_indices, float* debug_scores,
-                      const StatsPlan& p, int bh, hipStream_t st);
+                      const StatsPlan& p, int bh, hipStream_t st, int32_t dtype = 0,
+                      const pisa::ReduceArgs* fused_reduce = nullptr);
 
 static int prepare_impl(int32_t dtype, int32_t heads, int32_t tokens, int32_t head_dim, const pisa_view& q,
                         const pisa_view& k, const pisa_view& v, const pisa_token_grid& grid, int32_t exact_blocks,
@@ -341,13 +342,15 @@ static int prepare_impl(int32_t dtype, int32_t heads, int32_t tokens, int32_t he
     ra.vbar_t_pad = w.vbar_t_pad;
     ra.blocks = p.blocks;
     ra.npad = p.npad;
-    if ((rc = pisa::launch_stats_reduce(dtype, ra, bh, st))) return rc;
-    return route_impl(w, head_dim, exact_blocks, scale, sink_block, route_mode, debug_indices, debug_scores, p, bh, st);
+    // the routing workgroups also sum the H_sum partials (one launch)
+    return route_impl(w, head_dim, exact_blocks, scale, sink_block, route_mode, debug_indices, debug_scores, p, bh, st,
+                      dtype, &ra);
 }
 
 static int route_impl(const ForwardBuffers& w, int32_t head_dim, int32_t exact_blocks, float scale,
                       int32_t sink_block, int32_t route_mode, int32_t* debug_indices, float* debug_scores,
-                      const StatsPlan& p, int bh, hipStream_t st) {
+                      const StatsPlan& p, int bh, hipStream_t st, int32_t dtype,
+                      const pisa::ReduceArgs* fused_reduce) {
     int rc;
     pisa::RouteArgs ro;
     ro.qc = w.qc_route;
@@ -364,7 +367,9 @@ static int route_impl(const ForwardBuffers& w, int32_t head_dim, int32_t exact_b
     ro.scores = debug_scores;
     ro.selmask = w.selmask;
     ro.mask_words = p.mask_words;
-    if ((rc = pisa::launch_route(ro, st))) return rc;
+    if (fused_reduce) rc = pisa::launch_route_reduce(dtype, ro, *fused_reduce, st);
+    else rc = pisa::launch_route(ro, st);
+    if (rc) return rc;
     if (debug_indices && exact_blocks > 0) {
         if (hipMemcpyAsync(debug_indices, w.idx, (size_t)bh * p.blocks * exact_blocks * 4, hipMemcpyDeviceToDevice, st) !=
             hipSuccess)

@@ -43,6 +43,71 @@ struct ReduceArgs {
     int blocks, npad;
 };
 
+// One 32x32 tile (tile = 4 * row tile + column tile) of the H_sum reduction of
+// head bh, by 256 threads: the per-chunk partials are added in chunk order
+// (the sum does not depend on how the loads are batched), H_sum is written in
+// fp32 and its transpose as packed dtype fragments (both optional).
+// `tile_lds` is a 32 x 33 float array; the call ends with a barrier, so it can
+// be called again on the same array.
+template <typename T>
+__device__ inline void reduce_h_tile(const ReduceArgs& a, int bh, int tile, float (*tile_lds)[33], int t) {
+    constexpr int D = 128;
+    const int tr = tile >> 2;  // 32-row tile index
+    const int tc = tile & 3;   // 32-col tile index
+    const float* src = a.hpart + (int64_t)bh * a.chunks * D * D;
+    float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    int64_t off[4];
+#pragma unroll
+    for (int it = 0; it < 4; ++it) off[it] = (int64_t)(tr * 32 + it * 8 + (t >> 5)) * D + tc * 32 + (t & 31);
+    constexpr int kBatch = 8;
+    for (int ch0 = 0; ch0 < a.chunks; ch0 += kBatch) {
+        float x[kBatch][4];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u)
+#pragma unroll
+            for (int it = 0; it < 4; ++it)
+                x[u][it] = ch0 + u < a.chunks ? src[(int64_t)(ch0 + u) * D * D + off[it]] : 0.0f;
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u)
+#pragma unroll
+            for (int it = 0; it < 4; ++it)
+                if (ch0 + u < a.chunks) s[it] += x[u][it];
+    }
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+        if (a.hsum) a.hsum[(int64_t)bh * D * D + off[it]] = s[it];
+        tile_lds[it * 8 + (t >> 5)][t & 31] = s[it];
+    }
+    __syncthreads();
+    if (a.ht) {
+        T* ht = static_cast<T*>(a.ht) + (int64_t)bh * D * D;
+#pragma unroll
+        for (int it = 0; it < 4; ++it) {
+            const int lr = it * 8 + (t >> 5);  // output row = H column
+            const int lc = t & 31;
+            ht[kfrag_elem(tc * 32 + lr, tr * 32 + lc, D)] = from_f32<T>(tile_lds[lc][lr]);
+        }
+    }
+    __syncthreads();
+}
+
+// Zeroes the packed centroids past the last block of head bh (their scores
+// are masked to -inf, and a zero value keeps 0 * value finite in the PV
+// product); any number of threads, t = thread index, `stride` threads.
+template <typename T>
+__device__ inline void zero_centroid_pad(const ReduceArgs& a, int bh, int t, int stride = 256) {
+    constexpr int D = 128;
+    const int pad = a.npad - a.blocks;
+    const int64_t head_base = (int64_t)bh * a.npad * D;
+    for (int i = t; i < pad * D; i += stride) {
+        const int j = a.blocks + i / D;
+        const int d = i - (i / D) * D;
+        const int64_t base = head_base + (int64_t)(j & ~63) * D;
+        if (a.kbar_pad) static_cast<T*>(a.kbar_pad)[base + kfrag_elem(j & 63, d, D)] = T(0.0f);
+        if (a.vbar_t_pad) static_cast<T*>(a.vbar_t_pad)[base + vfrag_elem(j & 63, d)] = T(0.0f);
+    }
+}
+
 struct RouteArgs {
     const float* qc;     // [BH][N][D]
     const float* kc;     // [BH][N][D]
@@ -89,6 +154,9 @@ struct LayoutArgs {
 int launch_stats(int dtype, int mode, const StatsArgs& a, int bh_count, hipStream_t stream);
 int launch_stats_reduce(int dtype, const ReduceArgs& a, int bh_count, hipStream_t stream);
 int launch_route(const RouteArgs& a, hipStream_t stream);
+// Routing with the H_sum reduction of head dim 128 (stats_reduce_kernel's work,
+// `r`) done by the routing workgroups of each head before they score.
+int launch_route_reduce(int dtype, const RouteArgs& a, const ReduceArgs& r, hipStream_t stream);
 // Block means for the generic path at padded width `padded` (a.head_dim < 128 or > 128).
 int launch_stats_means(int dtype, int padded, const StatsArgs& a, int bh_count, hipStream_t stream);
 // `padded` = padded_head_dim(a.head_dim); dense (sparse = tail = false) or PISA (both true).

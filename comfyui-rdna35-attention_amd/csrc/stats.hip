@@ -268,63 +268,9 @@ __global__ __launch_bounds__(kStatsThreads) __attribute__((amdgpu_waves_per_eu(2
 
 template <typename T>
 __global__ __launch_bounds__(256) void stats_reduce_kernel(ReduceArgs a) {
-    constexpr int D = 128;
     __shared__ float tile[32][33];
-    const int bh = blockIdx.y;
-    const int tr = blockIdx.x >> 2;  // 32-row tile index
-    const int tc = blockIdx.x & 3;   // 32-col tile index
-    const int t = threadIdx.x;
-    const float* src = a.hpart + (int64_t)bh * a.chunks * D * D;
-    // 4 elements per thread; the partials of 8 chunks are loaded together and
-    // added in chunk order (the sum does not depend on the load batching)
-    float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    int64_t off[4];
-#pragma unroll
-    for (int it = 0; it < 4; ++it) off[it] = (int64_t)(tr * 32 + it * 8 + (t >> 5)) * D + tc * 32 + (t & 31);
-    constexpr int kBatch = 8;
-    for (int ch0 = 0; ch0 < a.chunks; ch0 += kBatch) {
-        float x[kBatch][4];
-#pragma unroll
-        for (int u = 0; u < kBatch; ++u)
-#pragma unroll
-            for (int it = 0; it < 4; ++it)
-                x[u][it] = ch0 + u < a.chunks ? src[(int64_t)(ch0 + u) * D * D + off[it]] : 0.0f;
-#pragma unroll
-        for (int u = 0; u < kBatch; ++u)
-#pragma unroll
-            for (int it = 0; it < 4; ++it)
-                if (ch0 + u < a.chunks) s[it] += x[u][it];
-    }
-#pragma unroll
-    for (int it = 0; it < 4; ++it) {
-        const int lr = it * 8 + (t >> 5);
-        const int lc = t & 31;
-        if (a.hsum) a.hsum[(int64_t)bh * D * D + off[it]] = s[it];
-        tile[lr][lc] = s[it];
-    }
-    __syncthreads();
-    if (a.ht) {
-        T* ht = static_cast<T*>(a.ht) + (int64_t)bh * D * D;
-#pragma unroll
-        for (int it = 0; it < 4; ++it) {
-            const int lr = it * 8 + (t >> 5);  // output row = H column
-            const int lc = t & 31;
-            ht[kfrag_elem(tc * 32 + lr, tr * 32 + lc, D)] = from_f32<T>(tile[lc][lr]);
-        }
-    }
-    if (blockIdx.x == 0) {
-        // zero the centroids past the last block: their scores are masked to
-        // -inf, and a zero value keeps 0 * value finite in the PV product
-        const int pad = a.npad - a.blocks;
-        const int64_t head_base = (int64_t)bh * a.npad * D;
-        for (int i = t; i < pad * D; i += 256) {
-            const int j = a.blocks + i / D;
-            const int d = i - (i / D) * D;
-            const int64_t base = head_base + (int64_t)(j & ~63) * D;
-            if (a.kbar_pad) static_cast<T*>(a.kbar_pad)[base + kfrag_elem(j & 63, d, D)] = T(0.0f);
-            if (a.vbar_t_pad) static_cast<T*>(a.vbar_t_pad)[base + vfrag_elem(j & 63, d)] = T(0.0f);
-        }
-    }
+    reduce_h_tile<T>(a, blockIdx.y, blockIdx.x, tile, threadIdx.x);
+    if (blockIdx.x == 0) zero_centroid_pad<T>(a, blockIdx.y, threadIdx.x);
 }
 
 // Block means of the generic path at head dims other than 128 (the
