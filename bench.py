@@ -13,6 +13,10 @@ Also measured in the same process:
   * the fused attention kernel alone (PisaPlan.attend, one launch), timed
     with HIP events on the stream it runs on -> roofline against dense bf16
     MFMA peak;
+  * the marginal cost of the exact tiles inside that kernel: attend at 47 and
+    at 23 exact blocks per query block on the same inputs (the tail and the
+    correction do the same work in both), so the difference / 24 is the time
+    of one exact 64-key tile step for the whole grid -> exact_tiles_marginal;
   * the dense exact attention kernel of this library on the same shape (the
     1.8x comparator of the north star);
   * the CPU oracle (oracle.pisa.hyd_forward) on a bounded sample of heads,
@@ -61,6 +65,7 @@ TOKENS = SIDE * SIDE
 BLOCK = 64
 BLOCKS = TOKENS // BLOCK
 EXACT = 23
+EXACT_PROBE = 47  # second exact-block count of the marginal exact-tile measurement
 PEAK_BF16_FLOPS = 2.5e15  # MI355X dense bf16 MFMA (no sparsity)
 PEAK_HBM_BYTES = 8.0e12
 BASELINE_MS = 25.121  # reference, gfx1151
@@ -79,6 +84,11 @@ def algorithmic_flops() -> dict:
     stats = bh * BLOCKS * 2 * BLOCK * HEAD_DIM * HEAD_DIM               # H_b per block
     routing = bh * BLOCKS * BLOCKS * 2 * HEAD_DIM
     return {"exact": exact, "tail": tail, "correction": correction, "stats": stats, "routing": routing}
+
+
+def flops_per_exact_step() -> int:
+    """FLOP of one more exact 64-key tile for every query block of every head."""
+    return BATCH * HEADS * BLOCKS * 4 * BLOCK * BLOCK * HEAD_DIM
 
 
 def time_gpu(fn, steps: int, warmup: int) -> float:
@@ -433,6 +443,28 @@ def main() -> int:
     attend_ms = time_gpu(plan.attend, args.steps, args.warmup)
     torch.testing.assert_close(out4.permute(0, 2, 1, 3).reshape(BATCH, TOKENS, -1), out, atol=0, rtol=0)
 
+    # marginal cost of the exact tiles inside the fused kernel: the same inputs
+    # with EXACT_PROBE exact blocks per query block; the tail always walks every
+    # centroid and the correction is fixed, so the attend-time difference is
+    # exact-tile work alone (EXACT_PROBE - EXACT more 64-key tiles per query block)
+    plan_probe = mi355x_pisa.PisaPlan(q, k, v, out4, EXACT_PROBE, scale, token_grid=(1, SIDE, SIDE))
+    plan_probe.prepare()
+    attend_probe_ms = time_gpu(plan_probe.attend, args.steps, args.warmup)
+    attend_ms_again = time_gpu(plan.attend, args.steps, args.warmup)  # same clock state as the probe
+    chunk_ms = (attend_probe_ms - attend_ms_again) / (EXACT_PROBE - EXACT)
+    chunk_flops = flops_per_exact_step()
+    exact_tiles = {
+        "method": f"attend time at {EXACT_PROBE} vs {EXACT} exact blocks per query block, same inputs; "
+                  f"exact-tile time = per-tile slope x {EXACT}",
+        "exact_blocks": [EXACT, EXACT_PROBE],
+        "attend_ms": [round(attend_ms_again, 4), round(attend_probe_ms, 4)],
+        "ms_per_tile_step": round(chunk_ms, 5),
+        "exact_tile_ms": round(chunk_ms * EXACT, 4),
+        "achieved": round(chunk_flops / (chunk_ms * 1e-3) / 1e12, 2),
+        "unit": "TFLOP/s",
+        "frac": round(chunk_flops / (chunk_ms * 1e-3) / PEAK_BF16_FLOPS, 4),
+    }
+
     # dense exact attention of this library on the same shape
     dense_ms = time_gpu(lambda: mi355x_pisa.dense_attention(q, k, v, scale, merged_output=True), args.steps,
                         max(1, args.warmup // 2))
@@ -468,6 +500,7 @@ def main() -> int:
         },
         "mfma_util_pct": round(100 * achieved / PEAK_BF16_FLOPS, 2),
         "exact_tile_tflops": round(flops["exact"] / (attend_ms * 1e-3) / 1e12, 2),
+        "exact_tiles_marginal": exact_tiles,
         "call_effective_tflops": round(total_flops / (call_ms * 1e-3) / 1e12, 2),
         "stages_ms": {"prepare": round(prepare_ms, 4), "attend": round(attend_ms, 4)},
         "first_call_ms": round(first_call_ms, 3),
