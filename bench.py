@@ -68,7 +68,7 @@ EXACT = 23
 EXACT_PROBE = 47  # second exact-block count of the marginal exact-tile measurement
 PEAK_BF16_FLOPS = 2.5e15  # MI355X dense bf16 MFMA (no sparsity)
 PEAK_HBM_BYTES = 8.0e12
-BASELINE_MS = 25.121  # reference, gfx1151
+BASELINE_MS = 25.121  # the reference's published C4 call time, measured on gfx1151
 METRIC = "PISA call ms + MFMA util %, bf16 B=2 H=16 T=9216 D=128, 23/144 blocks"
 COPY_BYTES = 1 << 30          # profile run: elementwise copy of 1 GiB (reads and writes COPY_BYTES)
 PROFILE_ATTENDS = 40
