@@ -130,29 +130,24 @@ __device__ __forceinline__ void probs_half(const f32x16 (&s)[NT], float c, const
 }
 
 // D is the padded head dim (padded_head_dim); a.head_dim <= D is the real
-// one.  A wave holds NT 32-row query tiles: both tiles of a 64-row block up to
-// D = 128, one tile (two waves per block) above, where the accumulators and
-// operands of 64 rows would not fit the 512 registers.
-template <typename T, int D, bool SPARSE, bool TAIL>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1)))
-void attention_kernel(AttnArgs a, const int32_t* __restrict__ sel, const uint32_t* __restrict__ selmask) {
-    // sel/selmask are a.idx/a.selmask passed as restrict-qualified arguments: the
-    // kernel never writes them, so their wave-uniform reads become scalar loads.
+// one.  A wave holds NT 32-row query tiles of query block qb of head bh, rows
+// 32(sub + nt) + col: both tiles of the 64-row block (NT = 2, sub = 0) up to
+// D = 128, or one tile (NT = 1, sub = 0 or 1, two waves per block) above,
+// where the accumulators and operands of 64 rows would not fit the 512
+// registers, and for the split blocks of the last round (attention_kernel).
+template <typename T, int D, int NT, bool SPARSE, bool TAIL>
+__device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int qb, int sub,
+                                                const int32_t* __restrict__ sel,
+                                                const uint32_t* __restrict__ selmask) {
     static_assert(D % 32 == 0 && D <= 256, "padded head dim");
+    static_assert(NT == 1 || (NT == 2 && D <= 128), "query tiles per wave");
     typedef typename Elem<T>::vec8 vec8;
-    constexpr int NT = D <= 128 ? 2 : 1;  // 32-row query tiles per wave
-    constexpr int SUBS = 2 / NT;          // waves per 64-row query block
     constexpr int KT = D / 16;
     constexpr int MD = D / 32;
     constexpr int64_t kBlockBytes = (int64_t)D * kBlock * sizeof(T);
     const int lane = threadIdx.x;
     const int half = lane >> 5;
     const int col = lane & 31;
-    const int work = xcd_remap(blockIdx.x, gridDim.x);
-    const int block_work = work / SUBS;
-    const int sub = work - block_work * SUBS;
-    const int bh = block_work / a.q_blocks;
-    const int qb = block_work - bh * a.q_blocks;
     const float c = a.scale_log2;
 
     // Token of row r of block j is block_base(j) + intra_offset(r); this
@@ -429,6 +424,51 @@ void attention_kernel(AttnArgs a, const int32_t* __restrict__ sel, const uint32_
     }
 }
 
+// One wavefront per work item.  Work items are query blocks (64 rows, NT = 2)
+// up to D = 128 and 32-row halves of query blocks (NT = 1) above.  Consecutive
+// work items run on the same XCD (xcd_remap), keeping a head's packed K/V in
+// that XCD's L2.
+//
+// Split last round (a.split_r > 0, D = 128): a grid of B query blocks on S
+// wave slots (one wave per SIMD) runs in ceil(B / S) rounds, and a last round
+// of r = B mod S blocks leaves S - r SIMDs idle for a whole block time.  With
+// 2r <= S the last r blocks of every XCD instead run as 2r one-tile waves
+// (NT = 1, ~0.6 of a block's time each) that fill the XCD's SIMDs.  Each XCD
+// takes a contiguous range of qx = B / 8 blocks: its first qx - r work items
+// are whole blocks, the following 2r the halves of the rest, dispatched last.
+template <typename T, int D, bool SPARSE, bool TAIL>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void attention_kernel(AttnArgs a, const int32_t* __restrict__ sel, const uint32_t* __restrict__ selmask) {
+    // sel/selmask are a.idx/a.selmask passed as restrict-qualified arguments: the
+    // kernel never writes them, so their wave-uniform reads become scalar loads.
+    if constexpr (D == 128) {
+        if (a.split_r > 0) {
+            const int xcd = blockIdx.x & 7;
+            const int local = blockIdx.x >> 3;
+            const int qx = a.q_blocks_total >> 3;
+            const int full = qx - a.split_r;
+            if (local < full) {
+                const int blk = xcd * qx + local;
+                const int bh = blk / a.q_blocks;
+                attention_block<T, D, 2, SPARSE, TAIL>(a, bh, blk - bh * a.q_blocks, 0, sel, selmask);
+            } else {
+                const int h = local - full;
+                const int blk = xcd * qx + full + (h >> 1);
+                const int bh = blk / a.q_blocks;
+                attention_block<T, D, 1, SPARSE, TAIL>(a, bh, blk - bh * a.q_blocks, h & 1, sel, selmask);
+            }
+            return;
+        }
+    }
+    constexpr int NT = D <= 128 ? 2 : 1;  // 32-row query tiles per wave
+    constexpr int SUBS = 2 / NT;          // waves per 64-row query block
+    const int work = xcd_remap(blockIdx.x, gridDim.x);
+    const int block_work = work / SUBS;
+    const int bh = block_work / a.q_blocks;
+    attention_block<T, D, NT, SPARSE, TAIL>(a, bh, block_work - bh * a.q_blocks, work - block_work * SUBS, sel,
+                                            selmask);
+}
+
 // ---- packed key and value blocks (kfrag_elem / vfrag_elem order at the
 // padded width D; dims >= d_real and rows >= kv_tokens are zero; block j
 // row r is token map(64 j + r)).  One workgroup per block: 64 rows x D of K
@@ -489,10 +529,31 @@ __global__ __launch_bounds__(256) void kv_pack_kernel(View k, View v, TokenMap m
     }
 }
 
+// Wave slots per XCD at one wave per SIMD (0 if the device does not split
+// evenly into 8 XCDs).
+static int xcd_slots() {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus % 8 != 0)
+        return 0;
+    return cus / 8 * 4;
+}
+
 template <typename T, int D, bool SPARSE, bool TAIL>
-int launch_attention_t(const AttnArgs& a, int bh_count, hipStream_t stream) {
+int launch_attention_t(const AttnArgs& a_in, int bh_count, hipStream_t stream) {
     constexpr int kSubs = D <= 128 ? 1 : 2;  // waves per query block
-    const int waves = bh_count * a.q_blocks * kSubs;
+    AttnArgs a = a_in;
+    a.q_blocks_total = bh_count * a.q_blocks;
+    a.split_r = 0;
+    int waves = a.q_blocks_total * kSubs;
+    if (D == 128 && a.q_blocks_total % 8 == 0) {
+        static const int slots = xcd_slots();
+        const int r = slots > 0 ? (a.q_blocks_total / 8) % slots : 0;
+        if (r > 0 && 2 * r <= slots) {
+            a.split_r = r;
+            waves = a.q_blocks_total + 8 * r;
+        }
+    }
     hipLaunchKernelGGL((attention_kernel<T, D, SPARSE, TAIL>), dim3(waves), dim3(64), 0, stream, a, a.idx, a.selmask);
     return pisa_host::check_launch("attention_kernel");
 }

@@ -141,6 +141,9 @@ struct AttnArgs {
     const char* ht;          // [BH] packed D x D (kfrag_elem), element (c, r) = H_sum[r][c]
     float corr_scale;        // s / T
     int head_dim;            // real head dim (<= the kernel's padded width)
+    // set by the launcher: query blocks of the grid, and blocks per XCD run as
+    // two one-tile halves in the last round (0: no split)
+    int q_blocks_total, split_r;
 };
 
 struct LayoutArgs {
