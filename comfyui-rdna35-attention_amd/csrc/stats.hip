@@ -12,7 +12,8 @@
 //     fp32 accumulation), its Frobenius norm, and accumulates H_b into a
 //     per-workgroup partial of H_sum held in the MFMA accumulators,
 //   * writes the key and value block packed as attention-kernel operand
-//     fragments (kfrag_elem / vfrag_elem) and the packed centroid chunks
+//     fragments (kfrag_elem / vfrag_elem; both staged in LDS so every wave
+//     store is one contiguous 1 KB fragment) and the packed centroid chunks
 //     used by the tail.
 // The partial H_sum of each workgroup is written once; stats_reduce_kernel
 // sums the partials in a fixed order, so H_sum is deterministic (the
@@ -28,6 +29,7 @@ namespace pisa {
 
 constexpr int kStatsThreads = 256;
 constexpr int kLdsRow = kBlock + 8;  // padded LDS row (elements) of a transposed block
+constexpr int kKRow = 128 + 8;       // padded LDS row (elements) of a raw key row
 
 // Element (row d, token position p) of a transposed block in LDS.  The 16-byte
 // chunks of a row are XOR-swizzled by (d / 8) % 8: the staging writes (rows 8
@@ -45,6 +47,7 @@ __global__ __launch_bounds__(kStatsThreads) __attribute__((amdgpu_waves_per_eu(2
     __shared__ __attribute__((aligned(16))) T lds_hi[D * kLdsRow];
     __shared__ __attribute__((aligned(16))) T lds_lo[D * kLdsRow];
     __shared__ __attribute__((aligned(16))) T lds_v[D * kLdsRow];
+    __shared__ __attribute__((aligned(16))) T lds_k[kBlock * kKRow];  // raw key rows of the block
     __shared__ float red[3][4][D];
     __shared__ float kmean[D];
     __shared__ float norm_part[4];
@@ -102,12 +105,12 @@ __global__ __launch_bounds__(kStatsThreads) __attribute__((amdgpu_waves_per_eu(2
         const float inv_len = 1.0f / static_cast<float>(len);
         vec8 qv[4], kv[4], vv[4];
         load_block(b, qv, kv, vv);
-        // ---- packed key block for the attention kernel (raw rows; rows past a
-        // short block are zero)
+        // ---- raw key rows to LDS (rows past a short block are zero); they are
+        // written out as packed key fragments after the next barrier, one
+        // contiguous 1 KB fragment per wave store
         if (a.kp_blocks) {
-            T* dst = static_cast<T*>(a.kp_blocks) + ((int64_t)bh * a.blocks + b) * D * kBlock;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) store8(dst + kfrag_elem(rq * 4 + r, c16 * 8, D), kv[r]);
+            for (int r = 0; r < 4; ++r) *reinterpret_cast<vec8*>(&lds_k[(rq * 4 + r) * kKRow + c16 * 8]) = kv[r];
         }
 
         // ---- column sums over this thread's 4 rows, then over the block
@@ -143,6 +146,21 @@ __global__ __launch_bounds__(kStatsThreads) __attribute__((amdgpu_waves_per_eu(2
             }
         }
         __syncthreads();
+        if (a.kp_blocks) {
+            // packed key block for the attention kernel: element id*8.. of the
+            // block is fragment f = id / 64 (rows 32(f/8).., dims 16(f%8)..),
+            // lane L = id % 64 (row 32(f/8) + L%32, dims + 8(L/32)) (kfrag_elem)
+            T* dst = static_cast<T*>(a.kp_blocks) + ((int64_t)bh * a.blocks + b) * D * kBlock;
+#pragma unroll
+            for (int it = 0; it < 4; ++it) {
+                const int id = it * kStatsThreads + t;
+                const int f = id >> 6;
+                const int L = id & 63;
+                const int key = (f >> 3) * 32 + (L & 31);
+                const int d = (f & 7) * 16 + (L >> 5) * 8;
+                store8(dst + id * 8, *reinterpret_cast<const vec8*>(&lds_k[key * kKRow + d]));
+            }
+        }
         if (t < D) {
             const int d = t;
             float mq = ((red[0][0][d] + red[0][1][d]) + red[0][2][d]) + red[0][3][d];
