@@ -212,15 +212,28 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
     const int n_chunks = n_exact + (TAIL ? a.npad / kBlock : 0);
     const int32_t* my_idx = SPARSE ? sel + ((int64_t)bh * a.q_blocks + qb) * a.exact : nullptr;
     const uint32_t* my_mask = TAIL ? selmask + ((int64_t)bh * a.q_blocks + qb) * a.mask_words : nullptr;
-    const char* kp_head = a.kp + (int64_t)bh * a.kv_blocks * kBlockBytes + lane * 16;
-    const char* vp_head = a.vp + (int64_t)bh * a.kv_blocks * kBlockBytes + lane * 16;
-    const char* kc_head = TAIL ? a.kbar + (int64_t)bh * a.npad * D * sizeof(T) + lane * 16 : nullptr;
-    const char* vc_head = TAIL ? a.vbar_t + (int64_t)bh * a.npad * D * sizeof(T) + lane * 16 : nullptr;
+    // Packed tables of this head as buffer resources: a chunk is addressed by a
+    // wave-uniform byte offset (scalar arithmetic), the lane part is a fixed
+    // vector offset, and reads past a table return zero.
+    constexpr int kRawFlags = 0x00020000;  // untyped 32-bit data format
+    const int tab_bytes = a.kv_blocks * (int)kBlockBytes;
+    const __amdgpu_buffer_rsrc_t kp_rs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(a.kp + (int64_t)bh * a.kv_blocks * kBlockBytes), (short)0, tab_bytes, kRawFlags);
+    const __amdgpu_buffer_rsrc_t vp_rs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(a.vp + (int64_t)bh * a.kv_blocks * kBlockBytes), (short)0, tab_bytes, kRawFlags);
+    const int cen_bytes = TAIL ? a.npad * D * (int)sizeof(T) : 0;
+    const __amdgpu_buffer_rsrc_t kc_rs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(TAIL ? a.kbar + (int64_t)bh * a.npad * D * sizeof(T) : a.kp), (short)0, cen_bytes, kRawFlags);
+    const __amdgpu_buffer_rsrc_t vc_rs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(TAIL ? a.vbar_t + (int64_t)bh * a.npad * D * sizeof(T) : a.vp), (short)0, cen_bytes, kRawFlags);
+    const int lane_off = lane * 16;
     // The first-order correction (head dim 128 only) needs the packed D x D
     // matrix (32 fragments): the last iteration loads it into kf (fragments
     // 0..15) and vf (16..31) in place of the next chunk.
     const bool first_order = TAIL && D == 128 && a.ht != nullptr;
-    const char* ht = first_order ? a.ht + (int64_t)bh * D * D * sizeof(T) + lane * 16 : nullptr;
+    const __amdgpu_buffer_rsrc_t ht_rs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(first_order ? a.ht + (int64_t)bh * D * D * sizeof(T) : a.kp), (short)0,
+        first_order ? D * D * (int)sizeof(T) : 0, kRawFlags);
     // Chunks past the end re-read the last one, so every iteration issues the
     // same loads (their results are never used).
     auto is_tail = [&](int x) { return TAIL && min(x, n_chunks - 1) >= n_exact; };
@@ -229,20 +242,27 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
         if (TAIL && x >= n_exact) return x - n_exact;
         return SPARSE ? my_idx[x] : x;
     };
-    auto kptr = [&](int x, int row) { return (is_tail(x) ? kc_head : kp_head) + row * kBlockBytes; };
-    auto vptr = [&](int x, int row) { return (is_tail(x) ? vc_head : vp_head) + row * kBlockBytes; };
+    struct Src {
+        __amdgpu_buffer_rsrc_t rs;
+        int off;  // wave-uniform byte offset of the chunk
+    };
+    auto kptr = [&](int x, int row) { return Src{is_tail(x) ? kc_rs : kp_rs, row * (int)kBlockBytes}; };
+    auto vptr = [&](int x, int row) { return Src{is_tail(x) ? vc_rs : vp_rs, row * (int)kBlockBytes}; };
+    auto ld_frag = [&](const Src& p, int frag) -> vec8 {
+        return __builtin_bit_cast(vec8, __builtin_amdgcn_raw_buffer_load_b128(p.rs, lane_off, p.off + frag * 1024, 0));
+    };
 
     vec8 kf[2][KT];   // kf[mt]: key fragments of the next half chunk that uses them
     vec8 vf[MD][4];   // value fragments; [.][0..1] first half, [.][2..3] second half
-    auto load_k_half = [&](vec8 (&k)[KT], const char* p, int mt) {
+    auto load_k_half = [&](vec8 (&k)[KT], const Src& p, int mt) {
 #pragma unroll
-        for (int t = 0; t < KT; ++t) k[t] = load8<vec8>(p + (mt * KT + t) * 1024);
+        for (int t = 0; t < KT; ++t) k[t] = ld_frag(p, mt * KT + t);
     };
-    auto load_v_half = [&](const char* p, int mt) {
+    auto load_v_half = [&](const Src& p, int mt) {
 #pragma unroll
         for (int md = 0; md < MD; ++md)
 #pragma unroll
-            for (int ss = 0; ss < 2; ++ss) vf[md][2 * mt + ss] = load8<vec8>(p + (md * 4 + 2 * mt + ss) * 1024);
+            for (int ss = 0; ss < 2; ++ss) vf[md][2 * mt + ss] = ld_frag(p, md * 4 + 2 * mt + ss);
     };
     auto scores_half = [&](const vec8 (&k)[KT], f32x16 (&s)[NT]) {
 #pragma unroll
@@ -317,8 +337,8 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
     if (n_chunks > 0) {
         row0 = table_row(0);
         row1 = table_row(1);
-        const char* k0 = kptr(0, row0);
-        const char* v0 = vptr(0, row0);
+        const Src k0 = kptr(0, row0);
+        const Src v0 = vptr(0, row0);
         // The loop sits inside this block: entered only after the query loads
         // have landed (the first scores use them), the compiler's wait counts
         // at the loop head cover just the chunk loads in flight.  The loads
@@ -336,9 +356,9 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
             const int row2 = table_row(cc + 2);
             const bool tail = is_tail(cc);
             const bool last = cc + 1 == n_chunks;
-            const char* kn = (first_order && last) ? ht : kptr(cc + 1, row1);
-            const char* vn = (first_order && last) ? ht + 16 * 1024 : vptr(cc + 1, row1);
-            const char* kn2 = (first_order && last) ? ht : kptr(cc + 2, row2);
+            const Src kn = (first_order && last) ? Src{ht_rs, 0} : kptr(cc + 1, row1);
+            const Src vn = (first_order && last) ? Src{ht_rs, 16 * 1024} : vptr(cc + 1, row1);
+            const Src kn2 = (first_order && last) ? Src{ht_rs, 0} : kptr(cc + 2, row2);
             vec8 pf[NT][2];
 
             // ---- first half: scores in sa (issued, masked and max-checked one half earlier)
