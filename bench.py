@@ -440,24 +440,25 @@ def main() -> int:
     out4 = out4.view(BATCH, TOKENS, HEADS, HEAD_DIM).permute(0, 2, 1, 3)
     plan = mi355x_pisa.PisaPlan(q, k, v, out4, EXACT, scale, token_grid=(1, SIDE, SIDE))
     prepare_ms = time_gpu(plan.prepare, args.steps, args.warmup)
-    attend_ms = time_gpu(plan.attend, args.steps, args.warmup)
-    torch.testing.assert_close(out4.permute(0, 2, 1, 3).reshape(BATCH, TOKENS, -1), out, atol=0, rtol=0)
-
     # marginal cost of the exact tiles inside the fused kernel: the same inputs
-    # with EXACT_PROBE exact blocks per query block; the tail always walks every
-    # centroid and the correction is fixed, so the attend-time difference is
-    # exact-tile work alone (EXACT_PROBE - EXACT more 64-key tiles per query block)
+    # with EXACT_PROBE exact blocks per query block, timed just before the
+    # EXACT run below (same clock state); the tail always walks every centroid
+    # and the correction is fixed, so the attend-time difference is exact-tile
+    # work alone (EXACT_PROBE - EXACT more 64-key tiles per query block)
     plan_probe = mi355x_pisa.PisaPlan(q, k, v, out4, EXACT_PROBE, scale, token_grid=(1, SIDE, SIDE))
     plan_probe.prepare()
     attend_probe_ms = time_gpu(plan_probe.attend, args.steps, args.warmup)
-    attend_ms_again = time_gpu(plan.attend, args.steps, args.warmup)  # same clock state as the probe
-    chunk_ms = (attend_probe_ms - attend_ms_again) / (EXACT_PROBE - EXACT)
+    plan.prepare()
+    attend_ms = time_gpu(plan.attend, args.steps, args.warmup)  # the last PISA attend launches of the run
+    torch.testing.assert_close(out4.permute(0, 2, 1, 3).reshape(BATCH, TOKENS, -1), out, atol=0, rtol=0)
+
+    chunk_ms = (attend_probe_ms - attend_ms) / (EXACT_PROBE - EXACT)
     chunk_flops = flops_per_exact_step()
     exact_tiles = {
         "method": f"attend time at {EXACT_PROBE} vs {EXACT} exact blocks per query block, same inputs; "
                   f"exact-tile time = per-tile slope x {EXACT}",
         "exact_blocks": [EXACT, EXACT_PROBE],
-        "attend_ms": [round(attend_ms_again, 4), round(attend_probe_ms, 4)],
+        "attend_ms": [round(attend_ms, 4), round(attend_probe_ms, 4)],
         "ms_per_tile_step": round(chunk_ms, 5),
         "exact_tile_ms": round(chunk_ms * EXACT, 4),
         "achieved": round(chunk_flops / (chunk_ms * 1e-3) / 1e12, 2),
