@@ -162,13 +162,14 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
     {
         const char* q_head = a.q.data + a.q.row(bh, 0) * (int64_t)sizeof(T) + half * 16;
         const int base = a.qmap.block_base(qb);
+        const bool all_dims = a.head_dim >= D;  // else dims past the real head dim read as zero
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
             const int tok = min(base + q_off[nt], a.q_tokens - 1);  // rows past the end are never stored
             const char* p = q_head + (int64_t)tok * a.q.st * (int64_t)sizeof(T);
 #pragma unroll
             for (int t = 0; t < KT; ++t) {
-                if (D == 128 || t * 16 + half * 8 < a.head_dim) {
+                if (all_dims || t * 16 + half * 8 < a.head_dim) {
                     qreg[nt][t] = load8<vec8>(p + t * 32);
                 } else {
 #pragma unroll
@@ -430,7 +431,7 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 const int d = md * 32 + 8 * g + 4 * half;
-                if (D != 128 && d >= a.head_dim) continue;
+                if (d >= a.head_dim) continue;
                 vec4 out;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {

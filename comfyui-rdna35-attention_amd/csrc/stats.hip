@@ -73,6 +73,9 @@ __global__ __launch_bounds__(kStatsThreads) __attribute__((amdgpu_waves_per_eu(2
 
     // 4 rows x 8 dims of q, k, v of block b; rows past the end of a short last
     // block read a valid row and are zeroed (no branch around the loads).
+    // Issues the loads of 4 rows x 8 dims of q, k, v of block b (rows past the
+    // end of a short last block read a valid row; mask_block zeroes them once
+    // the loads are used, so issuing the loads does not wait for them).
     auto load_block = [&](int b, vec8 (&qv)[4], vec8 (&kv)[4], vec8 (&vv)[4]) {
         const int start = b * kBlock;
         const int len = min(kBlock, a.tokens - start);
@@ -85,6 +88,8 @@ __global__ __launch_bounds__(kStatsThreads) __attribute__((amdgpu_waves_per_eu(2
             kv[r] = load8<vec8>(a.k.data + a.k.row(bh, raster) * sizeof(T) + off);
             vv[r] = load8<vec8>(a.v.data + a.v.row(bh, raster) * sizeof(T) + off);
         }
+    };
+    auto mask_block = [&](int len, vec8 (&qv)[4], vec8 (&kv)[4], vec8 (&vv)[4]) {
 #pragma unroll
         for (int r = 0; r < 4; ++r)
             if (rq * 4 + r >= len)
@@ -97,14 +102,27 @@ __global__ __launch_bounds__(kStatsThreads) __attribute__((amdgpu_waves_per_eu(2
     };
 
     // Two workgroups share each CU (at most 256 registers per lane), so one
-    // workgroup's loads overlap the other's reductions and MFMAs; a register
-    // prefetch of the next block would not fit that budget.
+    // workgroup's loads overlap the other's reductions and MFMAs; within a
+    // workgroup the next block's rows are loaded once this block is staged in
+    // LDS, beside the H_b MFMAs and the packed value stores.
+    vec8 qv[4], kv[4], vv[4];
+    if (first < last) load_block(first, qv, kv, vv);
     for (int b = first; b < last; ++b) {
+        // per-thread indices re-derived every block: LDS and store addresses
+        // are recomputed where used instead of held in registers across the loop
+        int t_opaque = threadIdx.x;
+        asm volatile("" : "+v"(t_opaque));
+        const int t = t_opaque;
+        const int lane = t & 63;
+        const int wave = t >> 6;
+        const int half = lane >> 5;
+        const int col = lane & 31;
+        const int c16 = t & 15;
+        const int rq = t >> 4;
         const int start = b * kBlock;
         const int len = min(kBlock, a.tokens - start);
         const float inv_len = 1.0f / static_cast<float>(len);
-        vec8 qv[4], kv[4], vv[4];
-        load_block(b, qv, kv, vv);
+        mask_block(len, qv, kv, vv);
         // ---- raw key rows to LDS (rows past a short block are zero); they are
         // written out as packed key fragments after the next barrier, one
         // contiguous 1 KB fragment per wave store
@@ -189,6 +207,7 @@ __global__ __launch_bounds__(kStatsThreads) __attribute__((amdgpu_waves_per_eu(2
             if (a.vbar_t_pad) static_cast<T*>(a.vbar_t_pad)[chunk_base + vfrag_elem(b & 63, d)] = from_f32<T>(mv);
         }
         if (!kCov) {
+            if (b + 1 < last) load_block(b + 1, qv, kv, vv);
             __syncthreads();
             continue;
         }
@@ -217,6 +236,10 @@ __global__ __launch_bounds__(kStatsThreads) __attribute__((amdgpu_waves_per_eu(2
             if (MODE == PISA_STATS_HYD) *reinterpret_cast<vec4*>(&lds_lo[stage_off(d, p0)]) = l4;
             *reinterpret_cast<vec4*>(&lds_v[stage_off(d, p0)]) = v4;
         }
+        // the rows of this block are staged: the next block's loads fly during
+        // the H_b MFMAs and the packed value stores
+        __builtin_amdgcn_sched_barrier(0);
+        if (b + 1 < last) load_block(b + 1, qv, kv, vv);
         __syncthreads();
 
         // ---- H_b tile rows [32*wave, 32*wave+32) x all 128 columns, one
@@ -246,6 +269,9 @@ __global__ __launch_bounds__(kStatsThreads) __attribute__((amdgpu_waves_per_eu(2
                 ss += hb[v] * hb[v];
                 hp[nt][v] += hb[v];
             }
+            // one 32-column tile at a time: keeps the accumulators of a single
+            // tile live beside the next block's loads
+            __builtin_amdgcn_sched_barrier(0);
         }
         ss = wave_sum(ss);
         if (lane == 0) norm_part[wave] = ss;
@@ -390,6 +416,7 @@ int launch_stats_means_t(int padded, const StatsArgs& a, int bh_count, hipStream
     switch (padded) {
         case 64: hipLaunchKernelGGL((stats_means_kernel<T, 64>), grid, dim3(256), 0, stream, a); break;
         case 96: hipLaunchKernelGGL((stats_means_kernel<T, 96>), grid, dim3(256), 0, stream, a); break;
+        case 128: hipLaunchKernelGGL((stats_means_kernel<T, 128>), grid, dim3(256), 0, stream, a); break;  // 104..120
         case 160: hipLaunchKernelGGL((stats_means_kernel<T, 160>), grid, dim3(256), 0, stream, a); break;
         case 192: hipLaunchKernelGGL((stats_means_kernel<T, 192>), grid, dim3(256), 0, stream, a); break;
         case 256: hipLaunchKernelGGL((stats_means_kernel<T, 256>), grid, dim3(256), 0, stream, a); break;

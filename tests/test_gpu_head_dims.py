@@ -95,3 +95,35 @@ def test_dense_head_dim_strided_merged_output(native):
     out = native.dense_attention(q, k, v, 1 / math.sqrt(head_dim), merged_output=True)
     expected = oatt.dense_attention(np32(q), np32(k), np32(v)).transpose(0, 2, 1, 3).reshape(batch, tokens, -1)
     assert_close(np32(out), expected, 2e-2, 2e-2, "dense merged D=40")
+
+
+def _nan_padded(shape, head_dim, gen, dtype):
+    """[..., head_dim] views of [..., head_dim + 8] storage whose last 8 columns hold NaN."""
+    buf = torch.full((*shape, head_dim + 8), float("nan"), dtype=dtype)
+    buf[..., :head_dim] = torch.randn((*shape, head_dim), generator=gen).to(dtype)
+    return buf.cuda()[..., :head_dim]
+
+
+@pytest.mark.parametrize("head_dim", [104, 112, 120])
+def test_padded_128_head_dims_stay_inside_rows(native, head_dim):
+    """Head dims 104..120 run at the padded width 128.  The query dims past the real head dim are
+    read as zero (NaN stored after each row would reach every score otherwise) and the stores stop
+    at the real dims (the storage after each output row keeps its sentinel)."""
+    gen = torch.Generator().manual_seed(head_dim)
+    dtype = torch.bfloat16
+    q, k, v = (_nan_padded((2, 2, 200), head_dim, gen, dtype) for _ in range(3))
+    s = 1 / math.sqrt(head_dim)
+    out_buf = torch.full((2, 2, 200, head_dim + 8), 3.0, dtype=dtype, device="cuda")
+    print(f"dense D={head_dim} padded views", flush=True)
+    native._launch_dense(q, k, v, out_buf[..., :head_dim], s)
+    torch.cuda.synchronize()
+    expected = oatt.dense_attention(np32(q), np32(k), np32(v))
+    assert_close(np32(out_buf[..., :head_dim]), expected, TOL[dtype], TOL[dtype], f"dense D={head_dim}")
+    assert bool((out_buf[..., head_dim:] == 3.0).all()), "stores past the real head dim"
+
+    print(f"generic D={head_dim} padded views", flush=True)
+    out = native.generic_forward(q, k, v, 2, s, False)
+    ref = opisa.generic_forward(*(np32(t).reshape(4, 200, head_dim) for t in (q, k, v)), 2, s,
+                                first_order=False, dtype="bf16")
+    assert_close(np32(out), ref.reshape(2, 2, 200, head_dim).transpose(0, 2, 1, 3), TOL[dtype], TOL[dtype],
+                 f"generic D={head_dim}")
