@@ -266,7 +266,7 @@ def run_workload(name: str, args) -> dict:
         result = _line(f"C2 exact full attention ms ({label}), bf16 B=2 H=16 Tq=9216 Tk={kv_tokens} D=128", ms, args,
                        {"workload": "dense_exact_attention", "batch": 2, "heads": 16, "q_tokens": 9216,
                         "kv_tokens": kv_tokens, "head_dim": 128},
-                       _mfma_roofline("kv_pack_kernel + attention_kernel (dense)", flops, ms),
+                       _mfma_roofline("kv_pack_kernel + attention_persistent_kernel (dense)", flops, ms),
                        data="synthetic: seeded 0.5*N(0,1)")
         if not args.no_cpu_baseline:
             rows = 1024 if name == "c2" else 9216
@@ -292,7 +292,7 @@ def run_workload(name: str, args) -> dict:
         result = _line(f"C3 MiniMax-H3 exact attention ms, bf16 B=1 H=56 T={tokens} D=128, strided QKV views", ms,
                        args, {"workload": "minimax_h3_strided", "batch": 1, "heads": 56, "tokens": tokens,
                               "head_dim": 128},
-                       _mfma_roofline("kv_pack_kernel + attention_kernel (dense, strided views)", flops, ms),
+                       _mfma_roofline("kv_pack_kernel + attention_persistent_kernel (dense, strided views)", flops, ms),
                        extra={"torch_sdpa_strided_ms": round(sdpa_ms, 3), "baseline_ms_gfx1151": published},
                        baseline_ms=published)
         if not args.no_cpu_baseline:
@@ -323,7 +323,7 @@ def run_workload(name: str, args) -> dict:
         result = _line("C5 video PISA call ms, bf16 B=1 H=40 T=32768 D=128 (16x32x64), 80/512 blocks", call_ms, args,
                        {"workload": "video_pisa_generic", "batch": 1, "heads": heads, "tokens": tokens,
                         "grid": list(grid), "head_dim": 128, "blocks": blocks, "exact_blocks": exact},
-                       _mfma_roofline("attention_kernel (exact tiles + tail + first-order + merge)",
+                       _mfma_roofline("attention_persistent_kernel (exact tiles + tail + first-order + merge)",
                                       flops_exact + flops_tail + flops_corr, attend_ms),
                        extra={"stages_ms": {"prepare": round(prepare_ms, 4), "attend": round(attend_ms, 4)},
                               "exact_tile_tflops": round(flops_exact / (attend_ms * 1e-3) / 1e12, 2)},
@@ -492,7 +492,7 @@ def main() -> int:
                    "grid": [1, SIDE, SIDE], "head_dim": HEAD_DIM, "blocks": BLOCKS, "exact_blocks": EXACT},
         "roofline": {
             "bound": "mfma",
-            "kernel": "attention_kernel (exact tiles + tail + first-order + merge)",
+            "kernel": "attention_persistent_kernel (exact tiles + tail + first-order + merge)",
             "achieved": round(achieved / 1e12, 2),
             "peak": PEAK_BF16_FLOPS / 1e12,
             "unit": "TFLOP/s",

@@ -4,6 +4,8 @@
 // One wavefront owns one 64-row query block (all four SIMDs of a CU run
 // independent query blocks, 1 wave per SIMD, up to 512 registers each; at
 // padded head dims above 128 two waves split the block into 32-row halves).
+// At head dim 128 the waves are persistent (attention_persistent_kernel) and
+// copy the next block's first operands to LDS while the current one runs.
 // The wave keeps its query rows in registers for the whole kernel and walks
 // one list of 64-key chunks, with the operands of chunk c+1 in flight while
 // chunk c is computed:
@@ -129,26 +131,61 @@ __device__ __forceinline__ void probs_half(const f32x16 (&s)[NT], float c, const
     }
 }
 
+// The block a persistent wave runs next (nt = 0: none): its query rows and the
+// key and value fragments of its first chunk are copied to the wave's LDS
+// while the current block runs.
+struct NextBlock {
+    int bh, qb, sub, nt;
+};
+typedef __attribute__((address_space(3))) char lds_char;
+constexpr int kWaitLgkm0 = 0xC07F;  // s_waitcnt lgkmcnt(0) (vmcnt, expcnt at their maximum)
+constexpr int kWaitVm0 = 0x0F70;    // s_waitcnt vmcnt(0) (lgkmcnt, expcnt at their maximum)
+
+// Direct-to-LDS copy of 16 bytes per lane: lane l's 16 bytes at gptr land at
+// LDS byte address lds_base + 16 l.  Written as inline asm so that the
+// compiler's memory-counter bookkeeping does not model it (it would fall back
+// to full waits in the chunk loop); its counts then include fewer operations
+// than are in flight, which only makes its waits stricter, and the callers
+// order the copy with explicit waits.
+// M0 (the LDS base of the copy) is reserved by the compiler, which warns about
+// clobbering it; no other code in these kernels uses M0.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void lds_copy16(const void* gptr, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                 :
+                 : "v"(gptr), "s"(lds_base)
+                 : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
 // D is the padded head dim (padded_head_dim); a.head_dim <= D is the real
 // one.  A wave holds NT 32-row query tiles of query block qb of head bh, rows
 // 32(sub + nt) + col: both tiles of the 64-row block (NT = 2, sub = 0) up to
 // D = 128, or one tile (NT = 1, sub = 0 or 1, two waves per block) above,
 // where the accumulators and operands of 64 rows would not fit the 512
 // registers, and for the split blocks of the last round (attention_kernel).
-template <typename T, int D, int NT, bool SPARSE, bool TAIL>
+template <typename T, int D, int NT, bool SPARSE, bool TAIL, bool PERSIST = false>
 __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int qb, int sub,
                                                 const int32_t* __restrict__ sel,
-                                                const uint32_t* __restrict__ selmask) {
+                                                const uint32_t* __restrict__ selmask,
+                                                lds_char* lds = nullptr, bool from_lds = false,
+                                                NextBlock next = NextBlock{0, 0, 0, 0}) {
     static_assert(D % 32 == 0 && D <= 256, "padded head dim");
     static_assert(NT == 1 || (NT == 2 && D <= 128), "query tiles per wave");
     typedef typename Elem<T>::vec8 vec8;
     constexpr int KT = D / 16;
     constexpr int MD = D / 32;
     constexpr int64_t kBlockBytes = (int64_t)D * kBlock * sizeof(T);
-    const int lane = threadIdx.x;
+    int lane_id = threadIdx.x;
+    // a persistent wave re-derives its lane terms per block rather than holding
+    // every lane-dependent offset in registers across blocks
+    if constexpr (PERSIST) asm volatile("" : "+v"(lane_id));
+    const int lane = lane_id;
     const int half = lane >> 5;
     const int col = lane & 31;
     const float c = a.scale_log2;
+    const bool all_dims = a.head_dim >= D;  // else dims past the real head dim read as zero
 
     // Token of row r of block j is block_base(j) + intra_offset(r); this
     // wave's rows are 32(sub + nt) + col.
@@ -159,10 +196,17 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
     // ---- query rows: qreg[nt][t] = Q[row nt][t*16+half*8 .. +7] (zero past
     // the real head dim), kept in registers for the whole kernel
     vec8 qreg[NT][KT];
-    {
+    if (PERSIST && from_lds) {
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+            for (int t = 0; t < KT; ++t)
+                qreg[nt][t] = __builtin_bit_cast(
+                    vec8, *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(
+                              lds + (nt * KT + t) * 1024 + lane * 16));
+    } else {
         const char* q_head = a.q.data + a.q.row(bh, 0) * (int64_t)sizeof(T) + half * 16;
         const int base = a.qmap.block_base(qb);
-        const bool all_dims = a.head_dim >= D;  // else dims past the real head dim read as zero
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
             const int tok = min(base + q_off[nt], a.q_tokens - 1);  // rows past the end are never stored
@@ -235,6 +279,45 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
     const __amdgpu_buffer_rsrc_t ht_rs = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(first_order ? a.ht + (int64_t)bh * D * D * sizeof(T) : a.kp), (short)0,
         first_order ? D * D * (int)sizeof(T) : 0, kRawFlags);
+    // Copies the next block's query rows (fragment nt*KT + t at 1 KB each), the
+    // key fragments of its first chunk (LDS + 16 KB) and the value fragments of
+    // that chunk's first half (LDS + 32 KB) to this wave's LDS.
+    const int next_row0 = (PERSIST && SPARSE && next.nt > 0 && n_exact > 0)
+                              ? sel[((int64_t)next.bh * a.q_blocks + next.qb) * a.exact] : 0;
+    auto prefetch_next = [&]() {
+        if (!PERSIST || next.nt == 0) return;
+        __builtin_amdgcn_s_waitcnt(kWaitLgkm0);  // this block's LDS reads have landed
+        const uint32_t lds_addr = (uint32_t)(uintptr_t)lds;
+        const char* nq = a.q.data + a.q.row(next.bh, 0) * (int64_t)sizeof(T) + half * 16;
+        const int nbase = a.qmap.block_base(next.qb);
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+            if (nt < next.nt) {
+                const int tok = min(nbase + a.qmap.intra_offset(32 * (next.sub + nt) + col), a.q_tokens - 1);
+                const char* p = nq + (int64_t)tok * a.q.st * (int64_t)sizeof(T);
+#pragma unroll
+                for (int t = 0; t < KT; ++t) lds_copy16(p + t * 32, lds_addr + (nt * KT + t) * 1024);
+            }
+        }
+        if (n_chunks > 0) {
+            const bool tail0 = TAIL && n_exact == 0;
+            const int row = tail0 ? 0 : min(max(next_row0, 0), a.kv_blocks - 1);
+            const char* src = (tail0 ? a.kbar + (int64_t)next.bh * a.npad * D * sizeof(T)
+                                     : a.kp + (int64_t)next.bh * a.kv_blocks * kBlockBytes) +
+                              (int64_t)row * kBlockBytes + lane_off;
+#pragma unroll
+            for (int f = 0; f < 2 * KT; ++f) lds_copy16(src + f * 1024, lds_addr + 16384 + f * 1024);
+            const char* vsrc = (tail0 ? a.vbar_t + (int64_t)next.bh * a.npad * D * sizeof(T)
+                                      : a.vp + (int64_t)next.bh * a.kv_blocks * kBlockBytes) +
+                               (int64_t)row * kBlockBytes + lane_off;
+#pragma unroll
+            for (int md = 0; md < MD; ++md)
+#pragma unroll
+                for (int ss = 0; ss < 2; ++ss)
+                    lds_copy16(vsrc + (md * 4 + ss) * 1024, lds_addr + 32768 + (md * 2 + ss) * 1024);
+        }
+    };
+
     // Chunks past the end re-read the last one, so every iteration issues the
     // same loads (their results are never used).
     auto is_tail = [&](int x) { return TAIL && min(x, n_chunks - 1) >= n_exact; };
@@ -345,13 +428,32 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
         // at the loop head cover just the chunk loads in flight.  The loads
         // after the first scores go out in the loop's order (K half 1, V half
         // 0, next K half 0, V half 1).
-        load_k_half(kf[0], k0, 0);
-        load_k_half(kf[1], k0, 1);
-        load_v_half(v0, 0);
+        if (PERSIST && from_lds) {
+#pragma unroll
+            for (int f = 0; f < 2 * KT; ++f)
+                kf[f / KT][f % KT] = __builtin_bit_cast(
+                    vec8, *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(
+                              lds + 16384 + f * 1024 + lane * 16));
+        } else {
+            load_k_half(kf[0], k0, 0);
+            load_k_half(kf[1], k0, 1);
+        }
+        if (PERSIST && from_lds) {
+#pragma unroll
+            for (int md = 0; md < MD; ++md)
+#pragma unroll
+                for (int ss = 0; ss < 2; ++ss)
+                    vf[md][ss] = __builtin_bit_cast(
+                        vec8, *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(
+                                  lds + 32768 + (md * 2 + ss) * 1024 + lane * 16));
+        } else {
+            load_v_half(v0, 0);
+        }
         pin_q();
         scores_half(kf[0], sa);
         load_k_half(kf[0], kptr(1, row1), 0);
         load_v_half(v0, 1);
+        prefetch_next();
         ca = check_half(0, row0, 0, sa, true);
         for (int cc = 0; cc < n_chunks; ++cc) {
             const int row2 = table_row(cc + 2);
@@ -382,6 +484,8 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
             row1 = row2;
         }
     }
+
+    if (n_chunks == 0) prefetch_next();
 
     // ---- epilogue: normalise, add the first-order correction one 32-dim
     // tile at a time (keeps only 32 extra accumulators live), store the real
@@ -431,7 +535,7 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 const int d = md * 32 + 8 * g + 4 * half;
-                if (d >= a.head_dim) continue;
+                if (!all_dims && d >= a.head_dim) continue;
                 vec4 out;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
@@ -443,6 +547,11 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
             }
         }
     }
+    // A persistent wave waits here until its stores are acknowledged and the
+    // copies for the next block have landed: the next block then reads its LDS
+    // safely and starts with no writes in flight (the compiler counts pending
+    // reads exactly only when no writes are pending alongside them).
+    if constexpr (PERSIST) __builtin_amdgcn_s_waitcnt(kWaitVm0);
 }
 
 // One wavefront per work item.  Work items are query blocks (64 rows, NT = 2)
@@ -488,6 +597,53 @@ void attention_kernel(AttnArgs a, const int32_t* __restrict__ sel, const uint32_
     const int bh = block_work / a.q_blocks;
     attention_block<T, D, NT, SPARSE, TAIL>(a, bh, block_work - bh * a.q_blocks, work - block_work * SUBS, sel,
                                             selmask);
+}
+
+// Persistent variant (D = 128, head dim 128, a grid that splits evenly into the
+// 8 XCDs): one wave per SIMD for the whole launch.  Slot j of XCD x (S
+// slots per XCD, qx = B / 8 blocks per XCD) runs blocks x*qx + j + S*it for
+// it < F = qx / S, then its share of the r = qx mod S blocks left: one-tile
+// halves of block x*qx + F*S + j/2 when 2r <= S (as attention_kernel's split),
+// else whole block x*qx + F*S + j for j < r.  While a block runs, the next
+// block's query rows and first chunk are copied to the wave's LDS (40 KB per
+// wave, 160 KB per CU; direct-to-LDS loads), so its prologue reads LDS instead
+// of waiting on HBM.
+template <typename T, bool SPARSE, bool TAIL>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void attention_persistent_kernel(AttnArgs a, const int32_t* __restrict__ sel, const uint32_t* __restrict__ selmask) {
+    constexpr int D = 128;
+    __shared__ __attribute__((aligned(1024))) char lds_buf[40 * 1024];
+    lds_char* const lds = (lds_char*)lds_buf;
+    const int xcd = blockIdx.x & 7;
+    const int j = blockIdx.x >> 3;
+    const int S = gridDim.x >> 3;
+    const int qx = a.q_blocks_total >> 3;
+    const int F = qx / S;
+    const int r = qx - F * S;
+    const bool split = 2 * r <= S;
+    const int n_items = F + ((split ? j < 2 * r : j < r) ? 1 : 0);
+    auto item = [&](int it) -> NextBlock {
+        if (it >= n_items) return NextBlock{0, 0, 0, 0};
+        int blk = xcd * qx + F * S + j, sub = 0, nt = 2;
+        if (it < F) {
+            blk = xcd * qx + j + S * it;
+        } else if (split) {
+            blk = xcd * qx + F * S + (j >> 1);
+            sub = j & 1;
+            nt = 1;
+        }
+        const int bh = blk / a.q_blocks;
+        return NextBlock{bh, blk - bh * a.q_blocks, sub, nt};
+    };
+    NextBlock cur = item(0);
+    for (int it = 0; it < n_items; ++it) {
+        const NextBlock nxt = item(it + 1);
+        if (cur.nt == 2)
+            attention_block<T, D, 2, SPARSE, TAIL, true>(a, cur.bh, cur.qb, 0, sel, selmask, lds, it > 0, nxt);
+        else
+            attention_block<T, D, 1, SPARSE, TAIL, true>(a, cur.bh, cur.qb, cur.sub, sel, selmask, lds, it > 0, nxt);
+        cur = nxt;
+    }
 }
 
 // ---- packed key and value blocks (kfrag_elem / vfrag_elem order at the
@@ -566,6 +722,14 @@ int launch_attention_t(const AttnArgs& a_in, int bh_count, hipStream_t stream) {
     AttnArgs a = a_in;
     a.q_blocks_total = bh_count * a.q_blocks;
     a.split_r = 0;
+    if constexpr (D == 128) {
+        static const int pslots = xcd_slots();
+        if (a.head_dim == D && a.q_blocks_total % 8 == 0 && pslots > 0) {
+            hipLaunchKernelGGL((attention_persistent_kernel<T, SPARSE, TAIL>), dim3(8 * pslots), dim3(64), 0, stream,
+                               a, a.idx, a.selmask);
+            return pisa_host::check_launch("attention_persistent_kernel");
+        }
+    }
     int waves = a.q_blocks_total * kSubs;
     if (D == 128 && a.q_blocks_total % 8 == 0) {
         static const int slots = xcd_slots();
