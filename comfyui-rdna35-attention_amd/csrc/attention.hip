@@ -384,18 +384,32 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
             }
             return c;
         }
-        // centroid jc = 64row + 32mt + bit: selected blocks and padding -> -inf,
-        // others + log2(len_jc) (scores moved to log2 units here)
+        // centroid jc = base + bit (base = 64row + 32mt): selected blocks and
+        // padding -> -inf, others + log2(len_jc) (scores moved to log2 units
+        // here).  One bias per accumulator row, shared by the query tiles: the
+        // dead bits of the half (selection word | padding) are one scalar word,
+        // shifted to this lane's rows once.
+        const int base = row * kBlock + mt * 32;
         const uint32_t word = (2 * row + mt < a.mask_words) ? my_mask[2 * row + mt] : 0u;
+        const int rem = a.centroids - base;  // live centroids of the half are bits 0 .. rem-1
+        const uint32_t live = rem >= 32 ? 0xffffffffu : (rem <= 0 ? 0u : (1u << rem) - 1u);
+        const uint32_t lane_dead = (word | ~live) >> (4 * half);
+        float bias[16];
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-            const int bit = 8 * (v >> 2) + 4 * half + (v & 3);
-            const int jc = row * kBlock + mt * 32 + bit;
-            const bool dead = jc >= a.centroids || ((word >> bit) & 1u);
-            const float bias = (jc == a.centroids - 1) ? a.last_len_log2 : 6.0f;  // log2(64)
-#pragma unroll
-            for (int nt = 0; nt < NT; ++nt) s[nt][v] = dead ? -__builtin_inff() : fmaf(s[nt][v], c, bias);
+            const int b = 8 * (v >> 2) + (v & 3);
+            const int dead = (int)(lane_dead << (31 - b)) >> 31;  // 0 or -1
+            bias[v] = __builtin_bit_cast(float, (dead & (int)0xff800000u) | (~dead & 0x40c00000));  // -inf or 6 = log2(64)
         }
+        if (rem >= 1 && rem <= 32) {  // the half holds the last centroid (bit rem - 1), whose block may be short
+#pragma unroll
+            for (int v = 0; v < 16; ++v)
+                if (8 * (v >> 2) + 4 * half + (v & 3) == rem - 1 && bias[v] == 6.0f) bias[v] = a.last_len_log2;
+        }
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) s[nt][v] = fmaf(s[nt][v], c, bias[v]);
         return 1.0f;
     };
 
@@ -455,34 +469,45 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
         load_v_half(v0, 1);
         prefetch_next();
         ca = check_half(0, row0, 0, sa, true);
-        for (int cc = 0; cc < n_chunks; ++cc) {
+        // One chunk step: half 0 of chunk cc (scores in sa) beside the scores of
+        // half 1, then half 1 beside the scores of the next chunk's half 0.  The
+        // last step (`last`, a constant in each inlined copy) has no next chunk:
+        // those scores are dead code, and its loads bring the packed H_sum^T
+        // fragments of the correction instead.
+        auto chunk_step = [&](int cc, bool last, bool half0_only) __attribute__((always_inline)) {
             const int row2 = table_row(cc + 2);
             const bool tail = is_tail(cc);
-            const bool last = cc + 1 == n_chunks;
             const Src kn = (first_order && last) ? Src{ht_rs, 0} : kptr(cc + 1, row1);
             const Src vn = (first_order && last) ? Src{ht_rs, 16 * 1024} : vptr(cc + 1, row1);
             const Src kn2 = (first_order && last) ? Src{ht_rs, 0} : kptr(cc + 2, row2);
             vec8 pf[NT][2];
 
             // ---- first half: scores in sa (issued, masked and max-checked one half earlier)
-            scores_half(kf[1], sb);
+            if (!half0_only) scores_half(kf[1], sb);
             probs_half<T, NT>(sa, ca, m, l, lt, tail, pf);
             load_k_half(kf[1], kn, 1);
             pv_half(0, pf);
             load_v_half(vn, 0);
-            const float cb = check_half(cc, row0, 1, sb, true);
+            const float cb = half0_only ? c : check_half(cc, row0, 1, sb, true);
 
             // ---- second half: scores in sb; also scores the next chunk's first half
-            // (past the end on the last iteration: computed, never used)
-            scores_half(kf[0], sa);
-            probs_half<T, NT>(sb, cb, m, l, lt, tail, pf);
+            if (!last) scores_half(kf[0], sa);
+            if (!half0_only) probs_half<T, NT>(sb, cb, m, l, lt, tail, pf);
             load_k_half(kf[0], kn2, 0);
-            pv_half(1, pf);
+            if (!half0_only) pv_half(1, pf);
             load_v_half(vn, 1);
-            ca = check_half(cc + 1, row1, 0, sa, !last);
+            if (!last) ca = check_half(cc + 1, row1, 0, sa, true);
             row0 = row1;
             row1 = row2;
-        }
+        };
+        for (int cc = 0; cc + 1 < n_chunks; ++cc) chunk_step(cc, false, false);
+        // The last chunk.  A centroid chunk whose second half holds only
+        // padding (centroids past the last block: C4's 144 centroids end 16 keys
+        // into their third chunk) skips that half's scores, softmax and PV
+        // (they would add exactly zero to l, l_tail and O); its loads still go
+        // out, unconditionally, so no register keeps two values across a branch.
+        const int cl = n_chunks - 1;
+        chunk_step(cl, true, TAIL && is_tail(cl) && table_row(cl) * kBlock + 32 >= a.centroids);
     }
 
     if (n_chunks == 0) prefetch_next();
