@@ -367,6 +367,10 @@ static int route_impl(const ForwardBuffers& w, int32_t head_dim, int32_t exact_b
     ro.scores = debug_scores;
     ro.selmask = w.selmask;
     ro.mask_words = p.mask_words;
+    const bool bf16_means = fused_reduce && route_mode == PISA_ROUTE_HYD && dtype == PISA_DTYPE_BF16 && head_dim == 128;
+    ro.qc_bf16 = bf16_means ? static_cast<const pisa::bf16_t*>(w.qc) : nullptr;
+    ro.kc_pack = bf16_means ? static_cast<const pisa::bf16_t*>(w.kbar_pad) : nullptr;
+    ro.npad = p.npad;
     if (fused_reduce) rc = pisa::launch_route_reduce(dtype, ro, *fused_reduce, st);
     else rc = pisa::launch_route(ro, st);
     if (rc) return rc;
@@ -549,6 +553,9 @@ int pisa_hip_route_topk(int32_t batch_heads, int32_t blocks, int32_t head_dim, c
     ro.scores = scores;
     ro.selmask = nullptr;
     ro.mask_words = 0;
+    ro.qc_bf16 = nullptr;
+    ro.kc_pack = nullptr;
+    ro.npad = 0;
     return pisa::launch_route(ro, static_cast<hipStream_t>(stream));
 }
 

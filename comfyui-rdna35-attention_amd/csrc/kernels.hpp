@@ -118,6 +118,12 @@ struct RouteArgs {
     float* scores;       // [BH][N][N] or null
     uint32_t* selmask;   // [BH][N][mask_words] or null
     int mask_words;
+    // HYD at head dim 128 with bf16 inputs: the bf16 means the statistics kernel
+    // wrote (q_bar row-major, k_bar as packed 64-centroid chunks), which equal
+    // the bf16 rounding of qc / kc; scored on bf16 MFMA when both are set
+    const bf16_t* qc_bf16;   // [BH][N][128] or null
+    const bf16_t* kc_pack;   // [BH][npad/64] packed chunks or null
+    int npad;
 };
 
 struct AttnArgs {

@@ -1,12 +1,14 @@
 // HYD and centroid routing scores and per-query-block top-k selection.
 //
-// One 256-thread workgroup owns 32 routing rows (query blocks i) of one
-// (batch, head).  Scores S[i][j] = q_i . k_j for every key block j are 32 x 32
-// tiles of fp32 MFMA (v_mfma_f32_32x32x2_f32), one tile per wave at a time,
-// written to LDS; the inputs are rounded to bf16 first for HYD, so every
-// product is exact and only the fp32 summation order is the hardware's.  Then
-// each wave selects 8 rows: lane l holds the candidates j = l, l+64, ... of a
-// row (scale, HYD bias ln(h_norm + 1e-5), sink override +inf).
+// One 256-thread workgroup owns 16 routing rows (query blocks i) of one
+// (batch, head).  Scores S[i][j] = q_i . k_j for every key block j are 16 x 16
+// tiles of MFMA written to LDS: for HYD with bf16 inputs the bf16 means the
+// statistics kernel wrote (which equal the bf16 rounding of the fp32 means) on
+// v_mfma_f32_16x16x32_bf16, otherwise the fp32 means on v_mfma_f32_16x16x4_f32
+// (rounded to bf16 first for HYD); every product is exact and only the fp32
+// summation order is the hardware's.  Then each wave selects 4 rows: lane l
+// holds the candidates j = l, l+64, ... of a row (scale, HYD bias
+// ln(h_norm + 1e-5), sink override +inf).
 //
 // With head dim 128 the same launch also carries the H_sum reduction
 // (reduce_h_tile): workgroups past the routing ones each sum two 32x32 tiles,
@@ -138,6 +140,44 @@ __global__ __launch_bounds__(64 * kRouteWaves) void route_topk_kernel(RouteArgs 
             for (int v = 0; v < 4; ++v) acc[v] = 0.0f;
         }
     };
+    if (a.qc_bf16 && a.kc_pack && D == 128) {
+        // bf16 means (HYD, bf16 inputs): 16x16x32 bf16 MFMA, lane (kg, c16)
+        // holding dims 32s + 8kg .. +7 of query row i0 + c16 (A) and of centroid
+        // ct*16 + c16 (B) for step s; products are exact, sums fp32.  All loads
+        // are unconditional (rows clamped; tiles past the wave's are formed but
+        // not stored), so the next tile's loads stay in flight while one tile is
+        // multiplied.
+        const bf16_t* qr = a.qc_bf16 + ((int64_t)bh * N + min(i0 + c16, N - 1)) * 128 + 8 * kg;
+        bf16x8 qf[4], kt[2][4];
+#pragma unroll
+        for (int st = 0; st < 4; ++st) qf[st] = *reinterpret_cast<const bf16x8*>(qr + 32 * st);
+        auto load_tile = [&](int m, bf16x8 (&kf)[4]) {
+            const int j = min((wave + kRouteWaves * min(m, my_tiles - 1)) * 16 + c16, N - 1);
+            const bf16_t* kr = a.kc_pack + ((int64_t)bh * a.npad + (j & ~63)) * 128;
+#pragma unroll
+            for (int st = 0; st < 4; ++st)
+                kf[st] = *reinterpret_cast<const bf16x8*>(kr + kfrag_elem(j & 63, 32 * st + 8 * kg, 128));
+        };
+        auto tile = [&](int m, const bf16x8 (&kf)[4]) {
+            f32x4 c4 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int st = 0; st < 4; ++st) c4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qf[st], kf[st], c4, 0, 0, 0);
+            const int j = (wave + kRouteWaves * m) * 16 + c16;
+            if (j < N) {
+#pragma unroll
+                for (int v = 0; v < 4; ++v) s_lds[(4 * kg + v) * stride + j] = c4[v];
+            }
+        };
+        if (my_tiles > 0) {
+            load_tile(0, kt[0]);
+            for (int m = 0; m < my_tiles; m += 2) {
+                load_tile(m + 1, kt[1]);
+                tile(m, kt[0]);
+                load_tile(m + 2, kt[0]);
+                tile(m + 1, kt[1]);
+            }
+        }
+    } else {
     if (pieces > 0) fetch(0, qa[0], kb[0]);
     for (int x = 0; x < pieces; x += 2) {
         if (x + 1 < pieces) fetch(x + 1, qa[1], kb[1]);
@@ -146,6 +186,7 @@ __global__ __launch_bounds__(64 * kRouteWaves) void route_topk_kernel(RouteArgs 
             if (x + 2 < pieces) fetch(x + 2, qa[0], kb[0]);
             piece(x + 1, qa[1], kb[1]);
         }
+    }
     }
     __syncthreads();
 
