@@ -66,7 +66,7 @@ __device__ inline void reduce_h_tile(const ReduceArgs& a, int bh, int tile, floa
         for (int u = 0; u < kBatch; ++u)
 #pragma unroll
             for (int it = 0; it < 4; ++it)
-                x[u][it] = ch0 + u < a.chunks ? src[(int64_t)(ch0 + u) * D * D + off[it]] : 0.0f;
+                x[u][it] = src[(int64_t)min(ch0 + u, a.chunks - 1) * D * D + off[it]];  // unconditional
 #pragma unroll
         for (int u = 0; u < kBatch; ++u)
 #pragma unroll

@@ -99,6 +99,10 @@ __global__ __launch_bounds__(64 * kRouteWaves) void route_topk_kernel(RouteArgs 
     const int pieces = my_tiles * per_tile;
     const float* qrow = a.qc + ((int64_t)bh * N + min(i0 + c16, N - 1)) * D;
     const float* kbase = a.kc + (int64_t)bh * N * D;
+    // The loads are unconditional (addresses clamped into the row), so the
+    // compiler's wait counts stay exact and the next pieces' loads really stay
+    // in flight; dims past D are zeroed where the operands are used (mask_piece,
+    // only when D is not a multiple of 64).
     auto fetch = [&](int x, float (&qa)[16], float (&kb)[16]) {
         const int ct = wave + kRouteWaves * (x / per_tile);
         const int s0 = 16 * (x % per_tile);
@@ -106,10 +110,9 @@ __global__ __launch_bounds__(64 * kRouteWaves) void route_topk_kernel(RouteArgs 
         if (wide) {
 #pragma unroll
             for (int p = 0; p < 4; ++p) {
-                const int d = 16 * (s0 / 4 + p) + 4 * kg;
-                const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
-                const f32x4 xq = d < D ? *reinterpret_cast<const f32x4*>(qrow + d) : z;
-                const f32x4 xk = d < D ? *reinterpret_cast<const f32x4*>(krow + d) : z;
+                const int d = min(16 * (s0 / 4 + p) + 4 * kg, D - 4);
+                const f32x4 xq = *reinterpret_cast<const f32x4*>(qrow + d);
+                const f32x4 xk = *reinterpret_cast<const f32x4*>(krow + d);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     qa[4 * p + e] = xq[e];
@@ -119,15 +122,28 @@ __global__ __launch_bounds__(64 * kRouteWaves) void route_topk_kernel(RouteArgs 
         } else {
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
-                const int d = 4 * (s0 + e) + kg;
-                qa[e] = d < D ? qrow[d] : 0.0f;
-                kb[e] = d < D ? krow[d] : 0.0f;
+                const int d = min(4 * (s0 + e) + kg, D - 1);
+                qa[e] = qrow[d];
+                kb[e] = krow[d];
+            }
+        }
+    };
+    const bool need_mask = D % 64 != 0;
+    auto mask_piece = [&](int x, float (&q)[16], float (&k)[16]) {
+        const int s0 = 16 * (x % per_tile);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int d = wide ? 16 * (s0 / 4 + e / 4) + 4 * kg + (e & 3) : 4 * (s0 + e) + kg;
+            if (d >= D) {
+                q[e] = 0.0f;
+                k[e] = 0.0f;
             }
         }
     };
     float qa[2][16], kb[2][16];
     f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    auto piece = [&](int x, const float (&q)[16], const float (&k)[16]) {
+    auto piece = [&](int x, float (&q)[16], float (&k)[16]) {
+        if (need_mask) mask_piece(x, q, k);
 #pragma unroll
         for (int e = 0; e < 16; ++e) acc = mfma16_f32(rnd ? round_bf16(q[e]) : q[e], rnd ? round_bf16(k[e]) : k[e], acc);
         if (x % per_tile == per_tile - 1) {  // tile done: acc[v] = S[i0 + 4 kg + v][ct * 16 + c16]
@@ -178,12 +194,15 @@ __global__ __launch_bounds__(64 * kRouteWaves) void route_topk_kernel(RouteArgs 
             }
         }
     } else {
-    if (pieces > 0) fetch(0, qa[0], kb[0]);
-    for (int x = 0; x < pieces; x += 2) {
-        if (x + 1 < pieces) fetch(x + 1, qa[1], kb[1]);
-        piece(x, qa[0], kb[0]);
-        if (x + 1 < pieces) {
-            if (x + 2 < pieces) fetch(x + 2, qa[0], kb[0]);
+    if (pieces > 0) {
+        // every step loads and multiplies (a piece index past the wave's last
+        // re-loads it; its tile lies past N and is not stored), so the count of
+        // loads after each operand's load is fixed and the waits stay exact
+        fetch(0, qa[0], kb[0]);
+        for (int x = 0; x < pieces; x += 2) {
+            fetch(min(x + 1, pieces - 1), qa[1], kb[1]);
+            piece(x, qa[0], kb[0]);
+            fetch(min(x + 2, pieces - 1), qa[0], kb[0]);
             piece(x + 1, qa[1], kb[1]);
         }
     }
