@@ -695,23 +695,30 @@ __global__ __launch_bounds__(256) void kv_pack_kernel(View k, View v, TokenMap m
     T* kdst = reinterpret_cast<T*>(kp) + ((int64_t)bh * kv_blocks + j) * D * kBlock;
     T* vdst = reinterpret_cast<T*>(vp) + ((int64_t)bh * kv_blocks + j) * D * kBlock;
     for (int r = r0 * 4; r < kBlock; r += kRowsPerPass * 4) {
-        vec8 x[4];
+        // the 8 loads of the 4 rows go out together and unconditionally (rows
+        // past kv_tokens re-read the last token, dims past d_real the first
+        // piece; both are zeroed at use), so no load waits behind another
+        vec8 kx[4], x[4];
+        bool live[4];
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
             const int key = j * kBlock + r + rr;
-            vec8 kx;
-            if (key < kv_tokens && live_d) {
-                const int tok = map(key);
-                kx = load8<vec8>(k.data + (k.row(bh, tok) + pc * 8) * sizeof(T));
-                x[rr] = load8<vec8>(v.data + (v.row(bh, tok) + pc * 8) * sizeof(T));
-            } else {
+            live[rr] = key < kv_tokens && live_d;
+            const int tok = map(min(key, kv_tokens - 1));
+            const int dc = live_d ? pc * 8 : 0;
+            kx[rr] = load8<vec8>(k.data + (k.row(bh, tok) + dc) * sizeof(T));
+            x[rr] = load8<vec8>(v.data + (v.row(bh, tok) + dc) * sizeof(T));
+        }
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+            if (!live[rr]) {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
-                    kx[e] = T(0.0f);
+                    kx[rr][e] = T(0.0f);
                     x[rr][e] = T(0.0f);
                 }
             }
-            store8(kdst + kfrag_elem(r + rr, pc * 8, D), kx);
+            store8(kdst + kfrag_elem(r + rr, pc * 8, D), kx[rr]);
         }
         const int p = swap23(r);
 #pragma unroll
