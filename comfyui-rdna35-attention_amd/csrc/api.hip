@@ -315,6 +315,10 @@ static int prepare_impl(int32_t dtype, int32_t heads, int32_t tokens, int32_t he
     sa.hnorm_out = w.hnorm;
     sa.hpart = w.hpart;
     sa.qc_route = w.qc_route;
+    // generic routing on HYD statistics multiplies the dtype-rounded q_bar with
+    // the fp32 k_bar (generic_pisa.py:120-126,172-173: block_stats_hyd returns
+    // q_bar in the input dtype, routed as q_bar.float())
+    sa.qc_route_round = (stats_mode == PISA_STATS_HYD && route_mode == PISA_ROUTE_CENTROID) ? 1 : 0;
     sa.kp_blocks = w.kp;
     sa.vp_blocks = w.vp;
     sa.kbar_pad = w.kbar_pad;

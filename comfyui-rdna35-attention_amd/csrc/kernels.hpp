@@ -22,6 +22,7 @@ struct StatsArgs {
     float* hpart;      // [BH][chunks][D][D] (HYD / GENERIC)
     // attention operands (nullable)
     float* qc_route;   // [BH][N][D] f32 means for routing
+    int qc_route_round;  // nonzero: the routing q_bar is the dtype-rounded mean (generic routing on HYD statistics)
     void* kp_blocks;   // [BH][N] packed key blocks (kfrag_elem order)
     void* vp_blocks;   // [BH][N] packed value blocks (vfrag_elem order)
     void* kbar_pad;    // [BH][npad/64] packed key chunks of dtype k_bar

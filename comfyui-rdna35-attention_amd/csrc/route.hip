@@ -305,7 +305,20 @@ static int launch_route_pl(const RouteArgs& a, const ReduceArgs& r, int fuse, hi
     const int row_tiles = (a.blocks + kRouteTile - 1) / kRouteTile;
     const int bh_count = a.rows / a.blocks;
     const dim3 grid(bh_count * row_tiles + (fuse ? bh_count * 8 : 0));  // routing, then reduction workgroups
-    const size_t lds = (size_t)kRouteTile * (a.blocks + 1) * sizeof(float);  // <= 64 KB for N <= 1024
+    // dynamic LDS: 16 score rows of N + 1 floats (65.6 KB at N = 1024, beside
+    // 4.2 KB of static LDS); gfx950 has 160 KB per workgroup, checked here
+    const size_t lds = (size_t)kRouteTile * (a.blocks + 1) * sizeof(float);
+    static const int lds_limit = [] {
+        int dev = 0, bytes = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&bytes, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
+            return 0;
+        return bytes;
+    }();
+    const size_t static_lds = sizeof(float) * 32 * 33;
+    if (lds_limit <= 0 || lds + static_lds > (size_t)lds_limit)
+        return pisa_host::fail(PISA_ERR_UNSUPPORTED, "routing over %d blocks needs %zu bytes of LDS, device allows %d",
+                               a.blocks, lds + static_lds, lds_limit);
     hipLaunchKernelGGL((route_topk_kernel<PL, T>), grid, dim3(64 * kRouteWaves), lds, stream, a, r, fuse);
     return PISA_OK;
 }

@@ -201,7 +201,7 @@ __global__ __launch_bounds__(kStatsThreads) __attribute__((amdgpu_waves_per_eu(2
             a.kc_out[o] = mk;
             if (a.vm_f32) static_cast<float*>(a.vm_out)[o] = mv;
             else static_cast<T*>(a.vm_out)[o] = from_f32<T>(mv);
-            if (a.qc_route) a.qc_route[o] = mq;
+            if (a.qc_route) a.qc_route[o] = a.qc_route_round ? to_f32(from_f32<T>(mq)) : mq;
             const int64_t chunk_base = ((int64_t)bh * a.npad + (b & ~63)) * D;  // packed 64-centroid chunk
             if (a.kbar_pad) static_cast<T*>(a.kbar_pad)[chunk_base + kfrag_elem(b & 63, d, D)] = from_f32<T>(mk);
             if (a.vbar_t_pad) static_cast<T*>(a.vbar_t_pad)[chunk_base + vfrag_elem(b & 63, d)] = from_f32<T>(mv);

@@ -96,6 +96,33 @@ def _validate_spatial_bhtd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) ->
         raise ValueError("PISA spatial HIP is forward-only.")
 
 
+def _check_inputs(what: str, q, k, v, *, dtypes, same_tokens: bool) -> None:
+    """Shape, dtype and device agreement of [B,H,T,D] q/k/v before any pointer reaches the C ABI.
+
+    k and v must match each other; q must share their batch, heads and head
+    dim, and their token count unless `same_tokens` is False (cross attention).
+    """
+    if not all(isinstance(tensor, torch.Tensor) for tensor in (q, k, v)):
+        raise TypeError(f"{what}: q, k, and v must be torch tensors.")
+    if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
+        raise ValueError(f"{what}: expects [B,H,T,D] q/k/v, got {q.ndim}-D/{k.ndim}-D/{v.ndim}-D")
+    if k.shape != v.shape:
+        raise ValueError(f"{what}: k {tuple(k.shape)} and v {tuple(v.shape)} must match")
+    if q.shape[0] != k.shape[0] or q.shape[1] != k.shape[1] or q.shape[3] != k.shape[3]:
+        raise ValueError(f"{what}: q {tuple(q.shape)} and k/v {tuple(k.shape)} must share batch, heads and head dim")
+    if same_tokens and q.shape[2] != k.shape[2]:
+        raise ValueError(f"{what}: q and k/v must have the same token count, got {q.shape[2]} and {k.shape[2]}")
+    if min(q.shape) <= 0 or min(k.shape) <= 0:
+        raise ValueError(f"{what}: every dimension must be positive")
+    if q.device != k.device or q.device != v.device or not _is_rocm_device(q):
+        raise ValueError(f"{what}: q/k/v must be on one PyTorch ROCm device.")
+    if q.dtype not in dtypes or k.dtype != q.dtype or v.dtype != q.dtype:
+        names = "/".join(str(d).replace("torch.", "") for d in dtypes)
+        raise ValueError(f"{what}: q/k/v must share one dtype of {names}, got {q.dtype}/{k.dtype}/{v.dtype}")
+    if q.stride(3) != 1 or k.stride(3) != 1 or v.stride(3) != 1:
+        raise ValueError(f"{what}: head_dim must have unit stride")
+
+
 def _check_exact_and_sink(exact_blocks, blocks: int, sink_block) -> None:
     if isinstance(exact_blocks, bool) or not isinstance(exact_blocks, int):
         raise TypeError("exact_blocks must be an integer.")
@@ -199,12 +226,29 @@ def _forward_impl(q, k, v, exact_blocks, scale, sink_block, token_grid=None, out
 
 
 # --------------------------------------------------------------------------- custom ops
-@torch.library.custom_op("mi355x_pisa::forward", mutates_args=(), device_types="cuda")
-def _forward_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, exact_blocks: int, scale: float,
-                sink_block: int) -> torch.Tensor:
+# Every op is a torch.library custom op with a fake implementation, so it
+# traces under torch.compile(fullgraph=True) (the reference registers its ops
+# the same way, __init__.py:197-213,319-378).  Eager calls on real tensors run
+# the kernel function directly: the custom op's first eager call imports
+# torch._dynamo (0.5-1 s of host time, during which the GPU idles), and an
+# eager caller gains nothing from the dispatcher.
+def _eager(*tensors) -> bool:
+    """True outside a compiler trace when every tensor is a plain torch.Tensor (not fake/functional)."""
+    if torch.compiler.is_compiling():
+        return False
+    return all(type(t) is torch.Tensor for t in tensors if t is not None)
+
+
+def _forward_kernel(q, k, v, exact_blocks: int, scale: float, sink_block: int) -> torch.Tensor:
     out = torch.empty_like(q)
     _forward_impl(_as4(q), _as4(k), _as4(v), exact_blocks, scale, sink_block, out4=_as4(out))
     return out
+
+
+@torch.library.custom_op("mi355x_pisa::forward", mutates_args=(), device_types="cuda")
+def _forward_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, exact_blocks: int, scale: float,
+                sink_block: int) -> torch.Tensor:
+    return _forward_kernel(q, k, v, exact_blocks, scale, sink_block)
 
 
 @_forward_op.register_fake
@@ -213,9 +257,7 @@ def _forward_op_fake(q, k, v, exact_blocks, scale, sink_block):
     return torch.empty_like(q)
 
 
-@torch.library.custom_op("mi355x_pisa::forward_spatial_bhtd", mutates_args=(), device_types="cuda")
-def _forward_spatial_bhtd_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, exact_blocks: int, scale: float,
-                             sink_block: int) -> torch.Tensor:
+def _forward_spatial_kernel(q, k, v, exact_blocks: int, scale: float, sink_block: int) -> torch.Tensor:
     batch, heads, tokens, head_dim = q.shape
     out = q.new_empty((batch, tokens, heads * head_dim))
     out4 = out.view(batch, tokens, heads, head_dim).permute(0, 2, 1, 3)
@@ -223,6 +265,12 @@ def _forward_spatial_bhtd_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, 
     token_grid = grid(1, SPATIAL_SIDE, SPATIAL_SIDE)
     _forward_impl(q, k, v, exact_blocks, scale, sink_block, token_grid=token_grid, out4=out4)
     return out
+
+
+@torch.library.custom_op("mi355x_pisa::forward_spatial_bhtd", mutates_args=(), device_types="cuda")
+def _forward_spatial_bhtd_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, exact_blocks: int, scale: float,
+                             sink_block: int) -> torch.Tensor:
+    return _forward_spatial_kernel(q, k, v, exact_blocks, scale, sink_block)
 
 
 @_forward_spatial_bhtd_op.register_fake
@@ -251,9 +299,8 @@ def _block_stats_hyd_op_fake(q, k, v):
     )
 
 
-@torch.library.custom_op("mi355x_pisa::generic_forward", mutates_args=(), device_types="cuda")
-def _generic_forward_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, exact_blocks: int, scale: float,
-                        first_order: bool, sink_block: int, frames: int, height: int, width: int) -> torch.Tensor:
+def _generic_forward_kernel(q, k, v, exact_blocks: int, scale: float, first_order: bool, sink_block: int,
+                            frames: int, height: int, width: int, stats_mode: int) -> torch.Tensor:
     batch, heads, tokens, head_dim = q.shape
     out = q.new_empty((batch, tokens, heads, head_dim))
     out4 = out.permute(0, 2, 1, 3)
@@ -262,19 +309,26 @@ def _generic_forward_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, exact
         _launch_dense(q, k, v, out4, scale)
     else:
         _launch_pisa(q, k, v, out4, grid(frames, height, width), exact_blocks, scale, sink_block,
-                     _lib.STATS_GENERIC, _lib.ROUTE_CENTROID, first_order)
+                     stats_mode, _lib.ROUTE_CENTROID, first_order)
     return out
 
 
+@torch.library.custom_op("mi355x_pisa::generic_forward", mutates_args=(), device_types="cuda")
+def _generic_forward_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, exact_blocks: int, scale: float,
+                        first_order: bool, sink_block: int, frames: int, height: int, width: int,
+                        stats_mode: int) -> torch.Tensor:
+    return _generic_forward_kernel(q, k, v, exact_blocks, scale, first_order, sink_block, frames, height, width,
+                                   stats_mode)
+
+
 @_generic_forward_op.register_fake
-def _generic_forward_op_fake(q, k, v, exact_blocks, scale, first_order, sink_block, frames, height, width):
-    del k, v, exact_blocks, scale, first_order, sink_block, frames, height, width
+def _generic_forward_op_fake(q, k, v, exact_blocks, scale, first_order, sink_block, frames, height, width,
+                             stats_mode):
+    del k, v, exact_blocks, scale, first_order, sink_block, frames, height, width, stats_mode
     return q.new_empty((q.shape[0], q.shape[2], q.shape[1], q.shape[3]))
 
 
-@torch.library.custom_op("mi355x_pisa::dense_attention", mutates_args=(), device_types="cuda")
-def _dense_attention_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float,
-                        merged_output: bool) -> torch.Tensor:
+def _dense_attention_kernel(q, k, v, scale: float, merged_output: bool) -> torch.Tensor:
     batch, heads, q_tokens, head_dim = q.shape
     if merged_output:
         out = q.new_empty((batch, q_tokens, heads * head_dim))
@@ -286,6 +340,12 @@ def _dense_attention_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale
     return out
 
 
+@torch.library.custom_op("mi355x_pisa::dense_attention", mutates_args=(), device_types="cuda")
+def _dense_attention_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float,
+                        merged_output: bool) -> torch.Tensor:
+    return _dense_attention_kernel(q, k, v, scale, merged_output)
+
+
 @_dense_attention_op.register_fake
 def _dense_attention_op_fake(q, k, v, scale, merged_output):
     del k, v, scale
@@ -295,12 +355,16 @@ def _dense_attention_op_fake(q, k, v, scale, merged_output):
     return q.new_empty((batch, heads, q_tokens, head_dim))
 
 
-@torch.library.custom_op("mi355x_pisa::fixed_block_attention", mutates_args=(), device_types="cuda")
-def _fixed_block_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float, causal: bool,
-                    mask: Optional[torch.Tensor]) -> torch.Tensor:
+def _fixed_block_kernel(q, k, v, scale: float, causal: bool, mask) -> torch.Tensor:
     out = q.new_empty(q.shape)
     _launch_fixed_block(q, k, v, out, scale, causal, mask)
     return out
+
+
+@torch.library.custom_op("mi355x_pisa::fixed_block_attention", mutates_args=(), device_types="cuda")
+def _fixed_block_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float, causal: bool,
+                    mask: Optional[torch.Tensor]) -> torch.Tensor:
+    return _fixed_block_kernel(q, k, v, scale, causal, mask)
 
 
 @_fixed_block_op.register_fake
@@ -356,6 +420,8 @@ def block_stats_hyd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor):
         raise ValueError("PISA HIP HYD requires contiguous q/k/v.")
     if q.requires_grad or k.requires_grad or v.requires_grad:
         raise ValueError("PISA HIP HYD is forward-only.")
+    if _eager(q, k, v):
+        return _block_stats(q, k, v, _lib.STATS_HYD, q.dtype)[:4]
     return _block_stats_hyd_op(q, k, v)[:4]
 
 
@@ -367,7 +433,8 @@ def forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, exact_blocks: int
     blocks = (q.shape[1] + BLOCK_SIZE - 1) // BLOCK_SIZE
     _check_exact_and_sink(exact_blocks, blocks, sink_block)
     scale_value = _float32(1.0 / math.sqrt(HEAD_DIM) if scale is None else scale)
-    return _forward_op(q, k, v, exact_blocks, scale_value, -2 if sink_block is None else sink_block)
+    fn = _forward_kernel if _eager(q, k, v) else _forward_op
+    return fn(q, k, v, exact_blocks, scale_value, -2 if sink_block is None else sink_block)
 
 
 def forward_spatial_bhtd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, exact_blocks: int,
@@ -391,23 +458,52 @@ def forward_spatial_bhtd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, exac
         )
     _check_exact_and_sink(exact_blocks, blocks, sink_block)
     scale_value = _float32(1.0 / math.sqrt(HEAD_DIM) if scale is None else scale)
-    return _forward_spatial_bhtd_op(q, k, v, exact_blocks, scale_value, -2 if sink_block is None else sink_block)
+    fn = _forward_spatial_kernel if _eager(q, k, v) else _forward_spatial_bhtd_op
+    return fn(q, k, v, exact_blocks, scale_value, -2 if sink_block is None else sink_block)
+
+
+# The generic path routes on the HYD statistics of the native module when that
+# module takes the shape (generic_pisa.py:106-126): head dim 128, bfloat16 (the
+# dtypes its capabilities list, __init__.py:472-473) and at most 9216 tokens
+# (its block_stats_hyd limit, __init__.py:30,219-220); otherwise on the
+# statistics of the Triton kernel (pisa_kernel.py:49-84).
+GENERIC_HYD_STATS_MAX_TOKENS = 9216
+
+
+def generic_stats_mode(tokens: int, head_dim: int, dtype: torch.dtype) -> str:
+    """'hyd' or 'generic': the statistics the reference's generic path uses for this shape."""
+    if head_dim == HEAD_DIM and dtype == torch.bfloat16 and 0 < tokens <= GENERIC_HYD_STATS_MAX_TOKENS:
+        return "hyd"
+    return "generic"
+
+
+_GENERIC_STATS = {"hyd": _lib.STATS_HYD, "generic": _lib.STATS_GENERIC}
 
 
 def generic_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, exact_blocks: int, scale: float,
                     first_order: bool, token_grid: tuple[int, int, int] | None = None,
-                    sink_block: int | None = None) -> torch.Tensor:
+                    sink_block: int | None = None, stats: str | None = None) -> torch.Tensor:
     """Generic PISA over [B,H,T,D] views (generic_pisa.py:141-232 semantics).
 
-    Centroid routing without the HYD bias, dtype-rounded centred keys for
-    H_sum, optional first-order correction.  token_grid=(frames, height, width)
-    selects per-frame 8x8 tile blocks; the output is [B,T,H,D] contiguous.
+    Centroid routing without the HYD bias, optional first-order correction.
+    `stats` picks the block statistics: "hyd" (dtype-rounded q_bar routed
+    against fp32 k_bar, keys centred in fp32), "generic" (fp32 means,
+    dtype-rounded centred keys) or None for the reference's own choice
+    (generic_stats_mode).  token_grid=(frames, height, width) selects per-frame
+    8x8 tile blocks; the output is [B,T,H,D] contiguous.
     """
+    _check_inputs("generic PISA", q, k, v, dtypes=(torch.bfloat16, torch.float16), same_tokens=True)
     frames, height, width = token_grid if token_grid is not None else (0, 0, 0)
     blocks = (q.shape[2] + BLOCK_SIZE - 1) // BLOCK_SIZE
     _check_exact_and_sink(exact_blocks, blocks, sink_block)
-    return _generic_forward_op(q, k, v, int(exact_blocks), _float32(scale), bool(first_order),
-                               -2 if sink_block is None else int(sink_block), int(frames), int(height), int(width))
+    mode = generic_stats_mode(q.shape[2], q.shape[3], q.dtype) if stats is None else stats
+    if mode not in _GENERIC_STATS:
+        raise ValueError("stats must be None, 'hyd' or 'generic'")
+    if mode == "hyd" and q.shape[3] != HEAD_DIM:
+        raise ValueError(f"HYD statistics require head_dim={HEAD_DIM}")
+    fn = _generic_forward_kernel if _eager(q, k, v) else _generic_forward_op
+    return fn(q, k, v, int(exact_blocks), _float32(scale), bool(first_order),
+              -2 if sink_block is None else int(sink_block), int(frames), int(height), int(width), _GENERIC_STATS[mode])
 
 
 def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float,
@@ -416,7 +512,9 @@ def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: fl
 
     Returns [B,H,Tq,D] contiguous, or [B,Tq,H*D] when merged_output is set.
     """
-    return _dense_attention_op(q, k, v, float(scale), bool(merged_output))
+    _check_inputs("dense attention", q, k, v, dtypes=(torch.bfloat16, torch.float16), same_tokens=False)
+    fn = _dense_attention_kernel if _eager(q, k, v) else _dense_attention_op
+    return fn(q, k, v, float(scale), bool(merged_output))
 
 
 def fixed_block_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float,
@@ -427,7 +525,17 @@ def fixed_block_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, sca
     (broadcast dims as 0 strides): bool keeps a score where True, a float mask
     is added to the scaled scores (reference.py:186-195).
     """
-    return _fixed_block_op(q, k, v, float(scale), bool(causal), mask)
+    _check_inputs("fixed-block attention", q, k, v, dtypes=(torch.bfloat16, torch.float16, torch.float32),
+                  same_tokens=True)
+    if mask is not None:
+        batch, heads, tokens, _ = q.shape
+        if not isinstance(mask, torch.Tensor) or mask.ndim != 4 or mask.device != q.device:
+            raise ValueError("fixed-block mask must be a 4-D tensor on q's device")
+        if tuple(mask.shape[2:]) != (tokens, tokens) or mask.shape[0] * mask.shape[1] != batch * heads:
+            raise ValueError(f"fixed-block mask must be [B',H',{tokens},{tokens}] with B'*H' = {batch * heads}, "
+                             f"got {tuple(mask.shape)}")
+    fn = _fixed_block_kernel if _eager(q, k, v, mask) else _fixed_block_op
+    return fn(q, k, v, float(scale), bool(causal), mask)
 
 
 def route_topk(q_centroids: torch.Tensor, k_centroids: torch.Tensor, h_norm: torch.Tensor | None,
@@ -437,7 +545,18 @@ def route_topk(q_centroids: torch.Tensor, k_centroids: torch.Tensor, h_norm: tor
 
     q/k centroids are fp32 [BH,N,D]; h_norm (fp32 [BH,N]) adds ln(h_norm+1e-5).
     """
+    if not isinstance(q_centroids, torch.Tensor) or not isinstance(k_centroids, torch.Tensor):
+        raise TypeError("centroids must be torch tensors")
+    if q_centroids.ndim != 3 or k_centroids.shape != q_centroids.shape:
+        raise ValueError("route_topk expects matching [BH,N,D] q/k centroids")
     bh, blocks, head_dim = q_centroids.shape
+    if h_norm is not None and tuple(h_norm.shape) != (bh, blocks):
+        raise ValueError(f"h_norm must be [BH,N] = [{bh},{blocks}]")
+    for tensor in (q_centroids, k_centroids, h_norm):
+        if tensor is not None and (tensor.device != q_centroids.device or not _is_rocm_device(tensor)):
+            raise ValueError("route_topk requires every tensor on one PyTorch ROCm device")
+    if isinstance(exact_blocks, bool) or not isinstance(exact_blocks, int) or not 0 <= exact_blocks <= blocks:
+        raise ValueError(f"exact_blocks must be an integer in [0,{blocks}]")
     qc = q_centroids.float().contiguous()
     kc = k_centroids.float().contiguous()
     hn = None if h_norm is None else h_norm.float().contiguous()
@@ -453,14 +572,26 @@ def route_topk(q_centroids: torch.Tensor, k_centroids: torch.Tensor, h_norm: tor
     return scores, indices[..., :exact_blocks]
 
 
+_ROUTING_MODES = {
+    "hyd": (_lib.STATS_HYD, _lib.ROUTE_HYD),                # __init__.py:233-316
+    "generic": (_lib.STATS_GENERIC, _lib.ROUTE_CENTROID),   # generic_pisa.py:128-138 statistics
+    "generic_hyd": (_lib.STATS_HYD, _lib.ROUTE_CENTROID),   # generic_pisa.py:120-126 statistics
+}
+
+
 def forward_with_routing(q4: torch.Tensor, k4: torch.Tensor, v4: torch.Tensor, exact_blocks: int, scale: float,
                          sink_block: int | None = None, hyd: bool = True, first_order: bool = True,
-                         token_grid: tuple[int, int, int] | None = None):
+                         token_grid: tuple[int, int, int] | None = None, mode: str | None = None):
     """Sparse PISA forward that also returns the routing scores and selection.
 
     Diagnostic entry point for parity checks: (out [B,H,T,D] contiguous,
-    scores fp32 [BH,N,N], indices int32 [BH,N,k]).
+    scores fp32 [BH,N,N], indices int32 [BH,N,k]).  `mode` is "hyd", "generic"
+    or "generic_hyd" (generic routing on HYD statistics); None takes `hyd`.
     """
+    _check_inputs("PISA", q4, k4, v4, dtypes=(torch.bfloat16, torch.float16), same_tokens=True)
+    mode = ("hyd" if hyd else "generic") if mode is None else mode
+    if mode not in _ROUTING_MODES:
+        raise ValueError(f"mode must be one of {sorted(_ROUTING_MODES)}")
     batch, heads, tokens, head_dim = q4.shape
     blocks = (tokens + BLOCK_SIZE - 1) // BLOCK_SIZE
     out = q4.new_empty(q4.shape)
@@ -468,8 +599,7 @@ def forward_with_routing(q4: torch.Tensor, k4: torch.Tensor, v4: torch.Tensor, e
     indices = torch.empty((batch * heads, blocks, max(exact_blocks, 1)), dtype=torch.int32, device=q4.device)
     frames, height, width = token_grid if token_grid is not None else (0, 0, 0)
     _launch_pisa(q4, k4, v4, out, grid(frames, height, width), exact_blocks, _float32(scale),
-                 -2 if sink_block is None else sink_block,
-                 _lib.STATS_HYD if hyd else _lib.STATS_GENERIC, _lib.ROUTE_HYD if hyd else _lib.ROUTE_CENTROID,
+                 -2 if sink_block is None else sink_block, *_ROUTING_MODES[mode],
                  first_order, debug_indices=indices, debug_scores=scores)
     return out, scores, indices[..., :exact_blocks]
 
@@ -571,26 +701,76 @@ def clear_compile_cache() -> None:
     """No run-time compilation happens; kept for API compatibility."""
 
 
+def _spatial_side(tokens: int) -> int:
+    side = math.isqrt(tokens)
+    if side * side != tokens or side % 8:
+        raise RuntimeError(f"spatial layouts need a square token grid with a side divisible by 8, got T={tokens}")
+    return side
+
+
+def _check_native(name: str, tensor, shape: tuple, dtypes: tuple, device=None) -> None:
+    """The reference's per-tensor TORCH_CHECKs of its native entry points (pisa_kernels.cu:719-745):
+    device tensor, exact shape, contiguous, dtype, forward-only.  Raised as RuntimeError."""
+    if not isinstance(tensor, torch.Tensor) or not _is_rocm_device(tensor):
+        raise RuntimeError(f"{name} must be a ROCm device tensor.")
+    if device is not None and tensor.device != device:
+        raise RuntimeError(f"{name} must be on {device}.")
+    if tuple(tensor.shape) != tuple(shape):
+        raise RuntimeError(f"{name} must have shape {list(shape)}, got {list(tensor.shape)}.")
+    if not tensor.is_contiguous():
+        raise RuntimeError(f"{name} must be contiguous.")
+    if tensor.dtype not in dtypes:
+        raise RuntimeError(f"{name} must be {' or '.join(str(d).replace('torch.', '') for d in dtypes)}.")
+    if tensor.requires_grad:
+        raise RuntimeError(f"{name} is forward-only.")
+
+
 class _NativeNamespace:
-    """The reference's pybind module surface (bindings.cpp:34-83) on HIP kernels."""
+    """The reference's pybind module surface (bindings.cpp:34-83) on HIP kernels.
+
+    Inputs are checked before any pointer reaches the C ABI, and tensors are
+    passed as they are (no temporary copies whose storage could be recycled
+    before the kernel runs)."""
 
     @staticmethod
     def build_info() -> dict[str, object]:
         return build_info()
 
     @staticmethod
+    def _stats_inputs(q, k, v):
+        if not all(isinstance(t, torch.Tensor) for t in (q, k, v)) or q.ndim != 3:
+            raise RuntimeError("block statistics expect matching [BH,T,D] q/k/v.")
+        for name, tensor in (("q", q), ("k", k), ("v", v)):
+            _check_native(name, tensor, tuple(q.shape), (torch.bfloat16, torch.float16), q.device)
+        if k.dtype != q.dtype or v.dtype != q.dtype:
+            raise RuntimeError("q, k, and v must have the same dtype.")
+        if q.shape[2] != HEAD_DIM or q.shape[0] <= 0 or q.shape[1] <= 0 or q.shape[1] > MAX_TOKENS:
+            raise RuntimeError(f"block statistics require BH>0, 0<T<={MAX_TOKENS}, and D={HEAD_DIM}.")
+
+    @staticmethod
     def block_stats(q, k, v):
+        _NativeNamespace._stats_inputs(q, k, v)
         return _block_stats(q, k, v, _lib.STATS_MEANS, q.dtype)
 
     @staticmethod
     def block_stats_hyd(q, k, v):
+        _NativeNamespace._stats_inputs(q, k, v)
         return _block_stats(q, k, v, _lib.STATS_HYD, q.dtype)
 
     @staticmethod
     def pack_spatial_qkv(q, k, v):
+        if not all(isinstance(t, torch.Tensor) for t in (q, k, v)) or q.ndim != 4:
+            raise RuntimeError("spatial QKV pack expects matching [B,H,T,D] q/k/v.")
+        for name, tensor in (("k", k), ("v", v)):
+            if tuple(tensor.shape) != tuple(q.shape) or tensor.device != q.device or tensor.dtype != q.dtype:
+                raise RuntimeError(f"{name} must match q in shape, dtype and device.")
+        if not _is_rocm_device(q) or q.dtype not in (torch.bfloat16, torch.float16):
+            raise RuntimeError("spatial QKV pack requires bf16/fp16 ROCm device tensors.")
+        if any(t.requires_grad for t in (q, k, v)):
+            raise RuntimeError("spatial QKV pack is forward-only.")
         batch, heads, tokens, head_dim = q.shape
+        side = _spatial_side(tokens)
         packed = [torch.empty((batch * heads, tokens, head_dim), dtype=q.dtype, device=q.device) for _ in range(3)]
-        side = math.isqrt(tokens)
         with torch.cuda.device(q.device):
             check(
                 LIB.pisa_hip_pack_spatial_qkv(
@@ -604,13 +784,19 @@ class _NativeNamespace:
 
     @staticmethod
     def unpack_spatial_output(output, batch, heads):
+        if not isinstance(output, torch.Tensor) or output.ndim != 3:
+            raise RuntimeError("spatial output unpack expects a [B*H,T,D] tensor.")
+        batch, heads = int(batch), int(heads)
+        if batch <= 0 or heads <= 0:
+            raise RuntimeError("spatial output unpack requires positive batch and heads.")
         bh, tokens, head_dim = output.shape
+        _check_native("output", output, (batch * heads, tokens, head_dim), (torch.bfloat16, torch.float16))
+        side = _spatial_side(tokens)
         out = output.new_empty((batch, tokens, heads * head_dim))
-        side = math.isqrt(tokens)
         with torch.cuda.device(output.device):
             check(
                 LIB.pisa_hip_unpack_spatial_output(
-                    dtype_code(output.dtype), batch, heads, tokens, head_dim, output.contiguous().data_ptr(),
+                    dtype_code(output.dtype), batch, heads, tokens, head_dim, output.data_ptr(),
                     grid(1, side, side), out.data_ptr(), stream_of(output.device),
                 ),
                 "pisa_hip_unpack_spatial_output",
@@ -619,16 +805,28 @@ class _NativeNamespace:
 
     @staticmethod
     def fuse_spatial_epilogue(exact_output, exact_lse, approximate_output, approximate_lse, correction, batch, heads):
-        bh, tokens, head_dim = exact_output.shape
+        if not isinstance(exact_output, torch.Tensor) or exact_output.ndim != 3:
+            raise RuntimeError("exact_output must have shape [B*H,T,D].")
+        batch, heads = int(batch), int(heads)
+        if batch <= 0 or heads <= 0:
+            raise RuntimeError("fused epilogue requires positive batch and heads.")
+        _, tokens, head_dim = exact_output.shape
+        rows = (batch * heads, tokens, head_dim)
+        device = exact_output.device
+        _check_native("exact_output", exact_output, rows, (torch.bfloat16, torch.float16), device)
+        _check_native("approximate_output", approximate_output, rows, (exact_output.dtype,), device)
+        _check_native("exact_lse", exact_lse, rows[:2], (torch.float32,), device)
+        _check_native("approximate_lse", approximate_lse, rows[:2], (torch.float32,), device)
+        _check_native("correction", correction, rows, (torch.float32,), device)
+        side = _spatial_side(tokens)
         out = exact_output.new_empty((batch, tokens, heads * head_dim))
-        side = math.isqrt(tokens)
-        with torch.cuda.device(exact_output.device):
+        with torch.cuda.device(device):
             check(
                 LIB.pisa_hip_fuse_spatial_epilogue(
                     dtype_code(exact_output.dtype), batch, heads, tokens, head_dim,
-                    exact_output.contiguous().data_ptr(), exact_lse.contiguous().data_ptr(),
-                    approximate_output.contiguous().data_ptr(), approximate_lse.contiguous().data_ptr(),
-                    correction.contiguous().data_ptr(), grid(1, side, side), out.data_ptr(), stream_of(exact_output.device),
+                    exact_output.data_ptr(), exact_lse.data_ptr(), approximate_output.data_ptr(),
+                    approximate_lse.data_ptr(), correction.data_ptr(), grid(1, side, side), out.data_ptr(),
+                    stream_of(device),
                 ),
                 "pisa_hip_fuse_spatial_epilogue",
             )
@@ -654,6 +852,7 @@ __all__ = [
     "forward_with_routing",
     "PisaPlan",
     "generic_forward",
+    "generic_stats_mode",
     "prepare",
     "route_topk",
 ]

@@ -82,19 +82,57 @@ def _unpack_video_blocks(tensor: torch.Tensor, grid_sizes) -> torch.Tensor:
 
 # ----------------------------------------------------------------------------- statistics / attention
 def _block_stats(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, return_backend: bool = False):
-    """(q_bar fp32, k_bar fp32, v_bar fp32, H_sum fp32, lengths) of [BH,T,D] q/k/v on the HIP statistics kernel.
+    """(q_bar, k_bar fp32, v_bar, H_sum fp32, lengths) of [BH,T,D] q/k/v on the HIP statistics kernel.
 
-    Generic semantics (generic_pisa.py:128-138): fp32 means, H_sum from centred
-    keys rounded to the input dtype.
+    The statistics the reference picks for the shape (generic_pisa.py:106-138):
+    the native HYD statistics at head dim 128, bfloat16, T <= 9216 (q_bar and
+    v_bar in the input dtype, keys centred in fp32; backend "hip_hyd"), else
+    the Triton semantics (fp32 means, centred keys rounded to the input dtype;
+    backend "hip_triton_stats").
     """
     native = diagnostics.load_native()
     tokens = q.shape[1]
     blocks = math.ceil(tokens / BLOCK_SIZE)
     lengths = torch.full((blocks,), BLOCK_SIZE, device=q.device, dtype=torch.float32)
     lengths[-1] = tokens - (blocks - 1) * BLOCK_SIZE
-    q_c, k_c, v_m, h_sum, _ = native._block_stats(q, k, v, 2, torch.float32)
+    if native.generic_stats_mode(tokens, q.shape[-1], q.dtype) == "hyd":
+        q_c, k_c, v_m, h_sum, _ = native._block_stats(q, k, v, native._lib.STATS_HYD, q.dtype)
+        backend = "hip_hyd"
+    else:
+        q_c, k_c, v_m, h_sum, _ = native._block_stats(q, k, v, native._lib.STATS_GENERIC, torch.float32)
+        backend = "hip_triton_stats"
     result = (q_c, k_c, v_m, h_sum, lengths)
-    return (*result, "hip_generic") if return_backend else result
+    return (*result, backend) if return_backend else result
+
+
+def _nonfinite(named) -> list[str]:
+    return [name for name, tensor in named if not torch.isfinite(tensor).all().item()]
+
+
+def _debug_stages(q, k, v, exact_blocks: int, scale: float, grid_sizes) -> None:
+    """debug_finite stage checks (generic_pisa.py:174-183,210-219).
+
+    The fused kernel never materialises the exact and approximate partial
+    outputs and LSEs, so the checks cover what exists separately: the block
+    statistics and the routing scores, recomputed here on the same inputs
+    (block-major order of the token grid; head dim 128, where the statistics
+    kernel runs on its own), then the fused output.
+    """
+    native = diagnostics.load_native()
+    if q.shape[2] != native.HEAD_DIM:  # the statistics kernel runs at head dim 128 only
+        return
+    q4, k4, v4 = (t.unsqueeze(1) for t in (q, k, v))
+    if grid_sizes is not None:
+        q4, k4, v4 = (_pack_video_blocks(t, grid_sizes) for t in (q4, k4, v4))
+    mode = native.generic_stats_mode(q.shape[1], q.shape[2], q.dtype)
+    if mode == "hyd":
+        q_c, k_c, v_m, _, _ = native._block_stats(q4, k4, v4, native._lib.STATS_HYD, q.dtype)
+    else:
+        q_c, k_c, v_m, _, _ = native._block_stats(q4, k4, v4, native._lib.STATS_GENERIC, torch.float32)
+    scores, _ = native.route_topk(q_c.float(), k_c, None, exact_blocks, scale, round_bf16=False)
+    failed = _nonfinite((("q_centroids", q_c), ("k_centroids", k_c), ("v_means", v_m), ("route_scores", scores)))
+    if failed:
+        raise ValueError(f"generic PISA non-finite stages: {','.join(failed)}")
 
 
 def generic_pisa_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, exact_budget: float,
@@ -104,6 +142,9 @@ def generic_pisa_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
 
     grid_sizes=(frames, height, width) declares a raster token grid; blocks are
     then its per-frame 8x8 tiles (the layout the reference obtains by packing).
+    Statistics follow the reference's choice for the shape (_block_stats); the
+    first-order term exists at head dim 128 (the only width whose statistics
+    kernel forms H_sum), so other widths need use_first_order=False.
     """
     if q.ndim != 3 or q.shape != k.shape or q.shape != v.shape:
         raise ValueError("generic PISA requires matching [BH,T,D] q/k/v")
@@ -115,21 +156,35 @@ def generic_pisa_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
         raise ValueError("generic PISA requires q/k/v on one CUDA/HIP device")
     if q.shape[-1] not in SUPPORTED_HEAD_DIMS:
         raise ValueError(f"generic PISA HIP kernels support head_dim {SUPPORTED_HEAD_DIMS}, got {q.shape[-1]}")
+    if use_first_order and q.shape[-1] != 128:
+        raise ValueError(f"generic PISA computes the first-order term at head_dim 128 only (got {q.shape[-1]}); "
+                         f"pass use_first_order=False")
     bh, tokens, head_dim = q.shape
     blocks = math.ceil(tokens / BLOCK_SIZE)
     exact_blocks = min(blocks, max(1, math.ceil(exact_budget * blocks)))
     s = float(scale) if scale is not None else 1.0 / math.sqrt(head_dim)
     native = diagnostics.load_native()
+    if debug_finite and exact_blocks < blocks:
+        _debug_stages(q, k, v, exact_blocks, s, grid_sizes)
     out = native.generic_forward(q.unsqueeze(1), k.unsqueeze(1), v.unsqueeze(1), exact_blocks, s, use_first_order,
                                  token_grid=grid_sizes)
     out = out.reshape(bh, tokens, head_dim)
-    if exact_blocks == blocks:
-        backend = "dense_hip"
-    else:
-        backend = "hip_generic" if use_first_order else "hip_generic_0th"
-    if debug_finite and not torch.isfinite(out).all().item():
-        raise ValueError("generic PISA non-finite stages: output")
+    backend = _backend_name(tokens, head_dim, q.dtype, exact_blocks == blocks, use_first_order)
+    if debug_finite:
+        failed = _nonfinite((("output", out),))
+        if failed:
+            raise ValueError(f"generic PISA non-finite stages: {','.join(failed)}")
     return (out, backend) if return_backend else out
+
+
+def _backend_name(tokens: int, head_dim: int, dtype, dense: bool, first_order: bool) -> str:
+    """hip_generic[_0th] on the Triton-semantics statistics, hip_generic_hyd[_0th] on the HYD ones
+    (the reference reports ck_hyd / triton_hyd and *_0th the same way, generic_pisa.py:231)."""
+    if dense:
+        return "dense_hip"
+    native = diagnostics.load_native()
+    name = "hip_generic_hyd" if native.generic_stats_mode(tokens, head_dim, dtype) == "hyd" else "hip_generic"
+    return name if first_order else name + "_0th"
 
 
 def make_generic_pisa_override(*, exact_budget: float, device_index: int, previous_override: Callable | None,
@@ -249,6 +304,4 @@ def _generic_pisa_bhtd(q4, k4, v4, exact_budget, scale, first_order, token_grid)
     s = float(scale) if scale is not None else 1.0 / math.sqrt(head_dim)
     native = diagnostics.load_native()
     out = native.generic_forward(q4, k4, v4, exact_blocks, s, first_order, token_grid=token_grid)
-    if exact_blocks == blocks:
-        return out, "dense_hip"
-    return out, "hip_generic" if first_order else "hip_generic_0th"
+    return out, _backend_name(tokens, head_dim, q4.dtype, exact_blocks == blocks, first_order)

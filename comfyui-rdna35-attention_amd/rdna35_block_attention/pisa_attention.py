@@ -184,8 +184,10 @@ def _run_hip(q, k, v, exact_count: int, scale: float, sink_block, hyd: bool) -> 
     native = diagnostics.load_native()
     if hyd:
         return native.forward(q, k, v, exact_count, scale=scale, sink_block=sink_block)
+    # the staged Triton backend's statistics (pisa_attention.py:314-320): fp32
+    # means, centred keys rounded to the input dtype
     out = native.generic_forward(q.unsqueeze(1), k.unsqueeze(1), v.unsqueeze(1), exact_count, scale, True,
-                                 sink_block=sink_block)
+                                 sink_block=sink_block, stats="generic")
     return out.reshape(q.shape)
 
 

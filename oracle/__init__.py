@@ -9,7 +9,7 @@ only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
 CPU fallback.
 
 Pinning (what fixes each function independently of its own formula; the
-tests live in tests/test_oracle_*.py):
+tests live in tests/test_oracle.py and tests/test_oracle_pins.py):
 
 * layout.ordered_to_raster / tile maps -- the reference's known answer
   (packed prefix [0..7, 96..103], test_forward.py:211-224), the torch
@@ -20,7 +20,20 @@ tests live in tests/test_oracle_*.py):
 * pisa.block_stats -- textbook means / covariance (float64), ||H_b||_F via
   numpy.linalg.norm, per-block-constant keys give H = 0, bf16 extrema stay
   finite (test_forward.py:172-201).
+* pisa.block_stats rounding points (tests/test_oracle_pins.py) -- exact rational
+  arithmetic with one fp32 rounding per step: the Triton statistics round the
+  centred keys to the dtype while HYD keeps them fp32; the means mode adds
+  x * fp32(1/len) with one fma per row (distinct from sum-then-scale and from
+  separately rounded products).
+* pisa.route_scores -- constructed inputs whose selection is fixed by
+  construction: q_bar orthogonal to every k_bar selects the largest textbook
+  ||H_b|| (presence and sign of the ln bias); equal ||H_b|| selects the top
+  q_bar . k_bar of a known table (no transpose); centroids whose bf16 and fp32
+  products rank differently pin where each path rounds (HYD: both centroids;
+  generic on HYD statistics: q_bar only; Triton statistics: neither).
 * pisa.topk_ascending -- brute-force ranking with explicit ties, sink and NaN.
+* layout.pack_minimax_h3_qkv -- the torch.stack copies at the 12000-token
+  threshold, bit for bit.
 * pisa.hyd_forward / generic_forward -- exact==N equals dense attention,
   constant V returns V, per-block-constant K makes the tail exact (no
   correction) and equals dense attention, and the LSE merge equals the

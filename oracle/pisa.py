@@ -44,17 +44,20 @@ def _block_view(x: np.ndarray, tokens: int) -> np.ndarray:
     return padded.reshape(bh, blocks, BLOCK, d)
 
 
-def block_stats(q: np.ndarray, k: np.ndarray, v: np.ndarray, mode: str = "hyd", dtype: str = "bf16") -> dict:
+def block_stats(q: np.ndarray, k: np.ndarray, v: np.ndarray, mode: str = "hyd", dtype: str = "bf16",
+                covariance: bool = True) -> dict:
     """Per-block statistics.
 
-    mode "means"  : every element pre-scaled by 1/len, then summed; q_bar and
-                    v_bar rounded to dtype, k_bar fp32 (pisa_kernels.cu:148-163).
+    mode "means"  : every element pre-scaled by 1/len while summing in row order
+                    (one fp32 fma per row); q_bar and v_bar rounded to dtype,
+                    k_bar fp32 (pisa_kernels.cu:148-163).
     mode "hyd"    : fp32 sums then * fp32(1/len); q_bar, v_bar rounded to dtype,
                     k_bar fp32; H_b = sum (k - k_bar)^T v with fp32 centring;
                     h_norm = ||H_b||_F; H_sum = sum_b H_b (pisa_kernels.cu:192-243).
     mode "generic": fp32 sums / len for all three (fp32 outputs); H_b from the
                     centred keys rounded to dtype (pisa_kernel.py:71-81,
                     generic_pisa.py:130-134).
+    covariance=False stops after the means (no H_b, h_norm or H_sum).
     """
     bh, tokens, d = q.shape
     lengths = block_lengths(tokens)
@@ -62,7 +65,15 @@ def block_stats(q: np.ndarray, k: np.ndarray, v: np.ndarray, mode: str = "hyd", 
     qb, kb, vb = (_block_view(x, tokens) for x in (q, k, v))
     out: dict = {"lengths": lengths}
     if mode == "means":
-        means = [f32(np.sum(f32(xb * inv[None, :, None, None]), axis=2)) for xb in (qb, kb, vb)]
+        # row by row, acc = fma(x, 1/len, acc): the kernel's `mean += x * inverse_length`
+        # (pisa_kernels.cu:148-158) as hipcc contracts it; x * inv is exact in float64
+        # (8 + 24 significant bits), so rounding the float64 sum is one fp32 fma
+        def prescaled_mean(xb):
+            acc = np.zeros(xb.shape[:2] + xb.shape[3:], dtype=np.float32)
+            for r in range(BLOCK):
+                acc = f32(acc.astype(np.float64) + xb[:, :, r] * inv[None, :, None].astype(np.float64))
+            return acc
+        means = [prescaled_mean(xb) for xb in (qb, kb, vb)]
         out["q_centroids"] = round_dtype(means[0], dtype)
         out["q_centroids_f32"] = means[0]
         out["k_centroids"] = means[1]
@@ -82,11 +93,13 @@ def block_stats(q: np.ndarray, k: np.ndarray, v: np.ndarray, mode: str = "hyd", 
     out["q_centroids_f32"] = means[0]
     k_mean = means[1]
     out["k_centroids"] = k_mean
+    if not covariance:  # means only (routing without the HYD bias needs nothing else)
+        return out
     valid = (np.arange(BLOCK)[None, :] < lengths[:, None])[None, :, :, None]
     centred = f32(np.where(valid, kb - k_mean[:, :, None, :].astype(np.float64), 0.0))
     if mode == "generic":
         centred = round_dtype(centred, dtype)
-    h_blocks = np.einsum("bnti,bntj->bnij", centred.astype(np.float64), vb)
+    h_blocks = np.matmul(np.swapaxes(centred.astype(np.float64), -1, -2), vb)  # sum_t centred[t,i] v[t,j]
     out["h_blocks"] = h_blocks
     out["h_norm"] = f32(np.sqrt(np.sum(h_blocks * h_blocks, axis=(-2, -1))))
     out["h_sum"] = f32(np.sum(h_blocks, axis=1))
@@ -274,16 +287,25 @@ def hyd_forward_concat(q, k, v, exact_blocks: int, scale: float | None = None, s
 
 
 def generic_forward(q, k, v, exact_blocks: int, scale: float | None = None, first_order: bool = True,
-                    dtype: str = "bf16", return_selection: bool = False):
-    """generic_pisa_attention (generic_pisa.py:141-232) with the Triton statistics path
-    (generic_pisa.py:128-138): fp32 centroids, no HYD bias, dtype-rounded centred keys."""
+                    dtype: str = "bf16", return_selection: bool = False, stats: str = "generic"):
+    """generic_pisa_attention (generic_pisa.py:141-232).
+
+    stats "generic": the Triton statistics path (generic_pisa.py:128-138,
+    pisa_kernel.py:71-81): fp32 centroids, dtype-rounded centred keys.
+    stats "hyd": the native block_stats_hyd path (generic_pisa.py:120-126),
+    taken by the reference for head dim 128, bfloat16 and T <= 9216: q_bar and
+    v_bar rounded to dtype, fp32 k_bar, keys centred in fp32.  Routing is
+    q_bar.float() . k_bar_fp32 * s in both (generic_pisa.py:172-173), with no
+    HYD bias; the tail uses dtype(k_bar) (generic_pisa.py:203-209)."""
     bh, tokens, d = q.shape
     blocks = (tokens + BLOCK - 1) // BLOCK
     s = 1.0 / math.sqrt(d) if scale is None else float(scale)
     if exact_blocks == blocks:
         out = dense_attention(q, k, v, s, out_dtype=dtype)
         return (out, None, None) if return_selection else out
-    st = block_stats(q, k, v, "generic", dtype)
+    if stats not in ("generic", "hyd"):
+        raise ValueError(stats)
+    st = block_stats(q, k, v, stats, dtype)
     lengths = st["lengths"]
     scores = route_scores(st["q_centroids"], st["k_centroids"], s, None, None, False)
     indices = topk_ascending(scores, exact_blocks)
@@ -314,11 +336,17 @@ def resolve_exact_blocks(total_blocks: int, exact_budget=None, sparsity=None, ex
 
 
 def reference_forward(q, k, v, exact_blocks: int, scale: float | None = None, sink_block: int | None = None,
-                      dtype: str = "bf16"):
+                      dtype: str = "bf16", centred_keys: str = "f32", return_selection: bool = False):
     """pisa_attention(backend="reference") (pisa_attention.py:73-185): fp32 block means,
     centroid routing without bias, exact online softmax over selected blocks, tail
     e^{s q.kbar_j} * sum(v_j) / (e^{s q.kbar_j} * len_j), first-order term
-    (q . H_sum * s/T) weighted by the tail denominator."""
+    (q . H_sum * s/T) weighted by the tail denominator.
+
+    centred_keys "f32" is the reference backend's H_sum (_reference_block_stats,
+    pisa_attention.py:73-91); "dtype" is the backend="triton" statistics
+    (pisa_prepare_triton, pisa_kernel.py:80-81: centred keys rounded to the
+    input dtype), which feed the same selection and piecewise forward
+    (pisa_attention.py:314-345)."""
     bh, tokens, d = q.shape
     blocks = (tokens + BLOCK - 1) // BLOCK
     s = 1.0 / math.sqrt(d) if scale is None else float(scale)
@@ -328,7 +356,12 @@ def reference_forward(q, k, v, exact_blocks: int, scale: float | None = None, si
     v_sums = f32(vb.sum(axis=2))
     valid = (np.arange(BLOCK)[None, :] < lengths[:, None])[None, :, :, None]
     centred = np.where(valid, kb - k_means[:, :, None, :].astype(np.float64), 0.0)
+    if centred_keys == "dtype":
+        centred = round_dtype(f32(centred), dtype).astype(np.float64)
+    elif centred_keys != "f32":
+        raise ValueError(centred_keys)
     h_sum = np.einsum("bnti,bntj->bij", centred, vb)
+    r = None
     if exact_blocks == blocks:
         selected = np.ones((bh, blocks, blocks), dtype=bool)
     elif exact_blocks == 0:
@@ -360,4 +393,6 @@ def reference_forward(q, k, v, exact_blocks: int, scale: float | None = None, si
         correction = np.einsum("btd,bde->bte", q_blk, h_sum) * (s / tokens)
         numerator += correction * tail_den[..., None]
         out[:, start:end] = numerator / denominator[..., None]
+    if return_selection:
+        return round_dtype(out, dtype), r, selected
     return round_dtype(out, dtype)

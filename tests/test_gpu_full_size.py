@@ -55,6 +55,33 @@ def test_c4_selection_bit_exact_and_oracle_heads(native, anima):
         assert_close(np32(out[b, h]), merged[0], 5e-2, 5e-2, f"C4 head {(b, h)}")
 
 
+def _selection_agreement(kernel_idx: np.ndarray, oracle_scores: np.ndarray, k: int, tol: float):
+    """Rows where the kernel's selection equals the oracle's, and whether every other row is a near-tie:
+    the oracle's k-th and (k+1)-th largest scores within `tol` (the routing-score tolerance), so that
+    a last-bit difference of the fp32 sums can swap the blocks at the boundary."""
+    expected = opisa.topk_ascending(oracle_scores, k)
+    equal = np.all(kernel_idx == expected, axis=-1)
+    ordered = -np.sort(-oracle_scores, axis=-1)
+    gap = ordered[..., k - 1] - ordered[..., k]
+    near_tie = gap <= tol * np.maximum(1.0, np.abs(ordered[..., k - 1]))
+    return equal, near_tie
+
+
+def test_c4_selection_agrees_with_the_oracle_on_every_head(native, anima):
+    """The kernel's selection against the oracle's own (oracle statistics -> oracle scores -> top-k)
+    for all 32 heads of C4: every row that differs must be a near-tie of the oracle's scores."""
+    q, k, v = anima
+    _, _, idx = native.forward_with_routing(q, k, v, 23, D ** -0.5, token_grid=(1, 96, 96))
+    packed = [spatial_to_packed(t, 1, 96, 96) for t in (q, k, v)]
+    st = opisa.block_stats(*packed, "hyd", "bf16")
+    scores = opisa.route_scores(st["q_centroids_f32"], st["k_centroids"], np.float32(D ** -0.5), st["h_norm"])
+    equal, near_tie = _selection_agreement(idx.cpu().numpy(), scores, 23, 1e-4)
+    print(f"C4 selection: {equal.sum()} / {equal.size} query blocks equal the oracle's "
+          f"({100.0 * equal.mean():.3f} %); differing rows that are near-ties: {near_tie[~equal].sum()}")
+    assert np.all(equal | near_tie)
+    assert equal.mean() >= 0.99
+
+
 def test_c4_constant_values_are_exact(native, anima):
     q, k, _ = anima
     v = torch.full_like(q, 0.3125)  # exactly representable; any convex combination returns it
@@ -141,3 +168,41 @@ def test_c5_video_selection_and_one_head(native):
     packed = [spatial_to_packed(t[:, 21:22], *grid) for t in (q, k, v)]
     expected = packed_to_merged(opisa.generic_forward(*packed, exact, dtype="bf16"), 1, 1, *grid)
     assert_close(np32(out[0, 21]), expected[0], 5e-2, 5e-2, "C5 head 21")
+    # the kernel's selection against the oracle's for all 40 heads (T = 32768 > 9216: the
+    # Triton-semantics statistics, fp32 means, generic_pisa.py:128-138)
+    assert native.generic_stats_mode(32768, D, torch.bfloat16) == "generic"
+    all_packed = [spatial_to_packed(t, *grid) for t in (q, k, v)]
+    st = opisa.block_stats(*all_packed, "generic", "bf16", covariance=False)
+    oracle_scores = opisa.route_scores(st["q_centroids"], st["k_centroids"], np.float32(D ** -0.5), None, None, False)
+    equal, near_tie = _selection_agreement(idx.cpu().numpy(), oracle_scores, exact, 1e-4)
+    print(f"C5 selection: {equal.sum()} / {equal.size} query blocks equal the oracle's "
+          f"({100.0 * equal.mean():.3f} %); differing rows that are near-ties: {near_tie[~equal].sum()}")
+    assert np.all(equal | near_tie)
+    assert equal.mean() >= 0.99
+
+
+@pytest.mark.parametrize("grid", [(2, 64, 64), (1, 64, 128), (8, 32, 32)])
+def test_wan_ltx_t8192_generic_routes_on_hyd_statistics(native, grid):
+    """Generic PISA at T = 8192, D = 128, bf16 (the Wan/LTX regime of README.md:110-112): the
+    reference routes on the native HYD statistics there (generic_pisa.py:120-126).  Selection
+    against the oracle's for every head, output against the oracle on two heads."""
+    from mi355x_pisa.synthetic import video_qkv
+
+    assert native.generic_stats_mode(8192, D, torch.bfloat16) == "hyd"
+    heads = 4
+    q, k, v = video_qkv(batch=1, heads=heads, grid=grid, seed=sum(grid), device="cuda")
+    exact = math.ceil(0.15625 * 128)
+    out, scores, idx = native.forward_with_routing(q, k, v, exact, D ** -0.5, token_grid=grid, mode="generic_hyd")
+    merged = native.generic_forward(q, k, v, exact, D ** -0.5, True, token_grid=grid)
+    assert torch.equal(merged.permute(0, 2, 1, 3), out)
+    np.testing.assert_array_equal(idx.cpu().numpy(), opisa.topk_ascending(np32(scores), exact))
+    packed = [spatial_to_packed(t, *grid) for t in (q, k, v)]
+    st = opisa.block_stats(*packed, "hyd", "bf16", covariance=False)
+    oracle_scores = opisa.route_scores(st["q_centroids"], st["k_centroids"], np.float32(D ** -0.5), None, None, False)
+    assert_close(np32(scores), oracle_scores, 1e-4, 1e-4, "T=8192 routing scores")
+    equal, near_tie = _selection_agreement(idx.cpu().numpy(), oracle_scores, exact, 1e-4)
+    assert np.all(equal | near_tie) and equal.mean() >= 0.99
+    for head in (0, 3):
+        one = [p[head:head + 1] for p in packed]
+        expected = packed_to_merged(opisa.generic_forward(*one, exact, dtype="bf16", stats="hyd"), 1, 1, *grid)
+        assert_close(np32(out[0, head]), expected[0], 5e-2, 5e-2, f"T=8192 head {head}")

@@ -110,8 +110,18 @@ def test_pisa_attention_triton_is_hip_centroid(dtype):
                                return_diagnostics=True)
     assert info["backend"] == "hip_centroid"
     name = "bf16" if dtype == torch.bfloat16 else "f16"
-    expected = opisa.generic_forward(np32(q), np32(k), np32(v), 3, dtype=name)
-    assert_close(np32(out), expected, 5e-2, 5e-2, "pisa centroid")
+    # the reference's staged Triton backend (pisa_attention.py:310-345): Triton statistics
+    # (dtype-rounded centred keys), fp32-mean selection, piecewise shared-normaliser forward
+    expected, ref_scores, ref_selected = opisa.reference_forward(np32(q), np32(k), np32(v), 3, dtype=name,
+                                                                 centred_keys="dtype", return_selection=True)
+    assert_close(np32(out), expected, 5e-2, 5e-2, "pisa triton backend")
+    import mi355x_pisa
+
+    _, scores, idx = mi355x_pisa.forward_with_routing(q.unsqueeze(1), k.unsqueeze(1), v.unsqueeze(1), 3, D ** -0.5,
+                                                      mode="generic")
+    assert_close(np32(scores), ref_scores, 1e-4, 1e-4, "triton backend routing scores")
+    kernel_selected = opisa.selection_mask(idx.cpu().numpy().astype(np.int64), ref_selected.shape[-1])
+    np.testing.assert_array_equal(kernel_selected, ref_selected)
     if dtype == torch.float16:
         _, auto = pisa_attention(q, k, v, exact_budget=0.5, return_diagnostics=True)
         assert auto["backend"] == "hip_centroid"
@@ -166,9 +176,10 @@ def test_generic_override_on_video_grid():
                                           previous_override=None, runtime_state=state)
     out = override(lambda *a, **kw: "original", *merged, heads, is_self_attention=True,
                    transformer_options={"grid_sizes": grid})
-    assert state.backend_counts["hip_generic"] == 1, state.report()
+    # T = 8192, D = 128, bf16: routed on the HYD statistics, as the reference (generic_pisa.py:120-126)
+    assert state.backend_counts["hip_generic_hyd"] == 1, state.report()
     packed = [spatial_to_packed(t, *grid) for t in (q4, k4, v4)]
-    expected = packed_to_merged(opisa.generic_forward(*packed, 20, dtype="bf16"), 1, heads, *grid)
+    expected = packed_to_merged(opisa.generic_forward(*packed, 20, dtype="bf16", stats="hyd"), 1, heads, *grid)
     assert_close(np32(out), expected, 5e-2, 5e-2, "generic video override")
 
 

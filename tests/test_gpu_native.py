@@ -352,7 +352,10 @@ def test_generic_forward_matches_oracle(native, grid, dtype, first_order):
     else:
         packed = [np32(t).reshape(2, tokens, D) for t in (q4, k4, v4)]
     name = "bf16" if dtype == torch.bfloat16 else "f16"
-    ref = opisa.generic_forward(*packed, exact, first_order=first_order, dtype=name)
+    # the statistics the reference's generic path takes for this shape (HYD for bf16 at T <= 9216)
+    stats = native.generic_stats_mode(tokens, D, dtype)
+    assert stats == ("hyd" if dtype == torch.bfloat16 else "generic")
+    ref = opisa.generic_forward(*packed, exact, first_order=first_order, dtype=name, stats=stats)
     if grid[0]:
         expected = packed_to_merged(ref, 1, 2, *grid)
     else:

@@ -284,3 +284,24 @@ def test_a_dropped_correction_is_detected():
     with_term = opisa.generic_forward(q, k, v, 1, first_order=True)
     without = opisa.generic_forward(q, k, v, 1, first_order=False)
     assert np.abs(with_term - without).max() > 5e-2
+
+
+# ----------------------------------------------------------------------------- fp32 torch CPU baseline
+@pytest.mark.parametrize("forward", ["hyd", "generic", "generic_hyd"])
+def test_torch_cpu_baseline_matches_the_oracle(forward):
+    """oracle.torch_cpu (the fp32 torch port timed as bench.py's cpu_baseline) against the float64
+    numpy oracle: same outputs within the bf16 tolerance on a short last block."""
+    from oracle import torch_cpu
+
+    rng = np.random.default_rng(11)
+    q, k, v = (round_bf16(rng.standard_normal((2, 1000, D)) * 0.7) for _ in range(3))
+    tq, tk, tv = (torch.from_numpy(x) for x in (q, k, v))
+    if forward == "hyd":
+        got = torch_cpu.hyd_forward(tq, tk, tv, 4).numpy()
+        expected = opisa.hyd_forward(q, k, v, 4)
+    else:
+        stats = "hyd" if forward == "generic_hyd" else "generic"
+        got = torch_cpu.generic_forward(tq, tk, tv, 4, stats=stats).numpy()
+        expected = opisa.generic_forward(q, k, v, 4, stats=stats)
+    np.testing.assert_allclose(got, expected, atol=5e-2, rtol=5e-2)
+    assert np.mean(np.abs(got - expected)) < 2e-3
