@@ -1,142 +1,122 @@
-"""Runtime detection used by the dispatch layers (reason strings, device gate).
+"""The gfx950 device gate and the HIP library loader.
 
-The reference probes Triton and RDNA3.5 targets (diagnostics.py:22-157); this
-build needs to know whether torch is a ROCm build, which gfx target the
-device is, and whether the gfx950 HIP library loads.
+Everything that decides whether a call may take the HIP path asks two
+questions, answered here: is this a gfx950 device of a ROCm PyTorch build,
+and does the gfx950 library (mi355x_pisa) load.  The package's public
+``detect_runtime`` / ``explain_dispatch`` (names of the reference's
+rdna35_block_attention/__init__.py:1-7) report exactly those facts.
 """
 from __future__ import annotations
 
-import importlib
-import os
 import re
 from typing import Any
 
+import torch
+
 TARGET = "gfx950"
-
-
-def _torch():
-    try:
-        return importlib.import_module("torch"), None
-    except Exception as exc:  # pragma: no cover - host without torch
-        return None, f"{type(exc).__name__}: {exc}"
-
-
-def is_rocm_pytorch() -> bool:
-    torch, _ = _torch()
-    return bool(torch is not None and getattr(getattr(torch, "version", None), "hip", None))
-
-
-def _cuda_available(torch) -> bool:
-    try:
-        return bool(torch.cuda.is_available())
-    except Exception:
-        return False
-
-
-def get_device_name(index: int = 0) -> str:
-    torch, error = _torch()
-    if torch is None:
-        return f"torch unavailable: {error}"
-    if not _cuda_available(torch):
-        return "cuda/hip device unavailable"
-    try:
-        return str(torch.cuda.get_device_name(index))
-    except Exception as exc:
-        return f"device name unavailable: {type(exc).__name__}: {exc}"
-
-
-def _gfx(value: Any) -> str | None:
-    match = re.search(r"gfx[0-9a-zA-Z]+", str(value)) if value is not None else None
-    return match.group(0) if match else None
-
-
-def best_effort_gfx_target(index: int = 0) -> str | None:
-    """gfx target from the usual build variables, else from the device properties."""
-    for name in ("PYTORCH_ROCM_ARCH", "GPU_ARCHS", "AMDGPU_TARGETS", "ROCM_ARCH"):
-        target = _gfx(os.environ.get(name))
-        if target:
-            return target
-    torch, _ = _torch()
-    if torch is None or not _cuda_available(torch):
-        return None
-    try:
-        props = torch.cuda.get_device_properties(index)
-    except Exception:
-        return None
-    for attr in ("gcnArchName", "gfx_version", "name"):
-        target = _gfx(getattr(props, attr, None))
-        if target:
-            return target
-    return None
-
-
-def device_gfx_target(device) -> str | None:
-    """gfx target of a concrete device, from its properties only."""
-    torch, _ = _torch()
-    if torch is None or not _cuda_available(torch):
-        return None
-    try:
-        return _gfx(getattr(torch.cuda.get_device_properties(device), "gcnArchName", None))
-    except Exception:
-        return None
-
-
-def native_status() -> tuple[bool, str]:
-    """(loaded, detail) of the gfx950 HIP library."""
-    try:
-        import mi355x_pisa
-
-        return True, str(mi355x_pisa.build_info().get("implementation"))
-    except Exception as exc:
-        return False, f"{type(exc).__name__}: {exc}"
 
 
 class NativeUnavailableError(RuntimeError):
     """The gfx950 HIP library is needed for an eligible call but cannot be loaded."""
 
 
+def _gfx(text: Any) -> str | None:
+    found = re.search(r"gfx[0-9a-z]+", str(text or ""))
+    return found.group(0) if found else None
+
+
+def is_rocm_pytorch() -> bool:
+    return torch.version.hip is not None
+
+
+def _have_device() -> bool:
+    try:
+        return torch.cuda.is_available()
+    except Exception:
+        return False
+
+
+def device_gfx_target(device) -> str | None:
+    """gfx target of a device from its properties (None without a visible ROCm device)."""
+    if not _have_device():
+        return None
+    try:
+        return _gfx(torch.cuda.get_device_properties(device).gcnArchName)
+    except Exception:
+        return None
+
+
+def gfx950_device_index() -> tuple[int | None, str | None]:
+    """(index of the current device, None) when it is a gfx950 under ROCm PyTorch, else (None, reason)."""
+    if not _have_device() or not is_rocm_pytorch():
+        return None, "PyTorch ROCm device is unavailable"
+    try:
+        index = torch.cuda.current_device()
+        target = device_gfx_target(index)
+    except (RuntimeError, AssertionError) as exc:
+        return None, f"could not query the current ROCm device ({type(exc).__name__}: {exc})"
+    if target != TARGET:
+        return None, f"{TARGET} is required, got {target or 'unknown'}"
+    return index, None
+
+
 def load_native():
-    """Import the HIP ops; raise NativeUnavailableError (never fall back) when they are missing."""
+    """The HIP op module; raises NativeUnavailableError (never falls back) when it cannot load."""
     try:
         import mi355x_pisa
     except Exception as exc:
-        raise NativeUnavailableError(f"the gfx950 HIP library (mi355x_pisa) is required on ROCm devices but failed to load: "
-                           f"{type(exc).__name__}: {exc}") from exc
+        raise NativeUnavailableError(f"the gfx950 HIP library (mi355x_pisa) is required on ROCm devices but failed "
+                                     f"to load: {type(exc).__name__}: {exc}") from exc
     return mi355x_pisa
 
 
+def native_status() -> tuple[bool, str]:
+    """(loaded, implementation or the load error) of the gfx950 HIP library."""
+    try:
+        return True, str(load_native().build_info().get("implementation"))
+    except Exception as exc:
+        return False, f"{type(exc).__name__}: {exc}"
+
+
+def get_device_name(index: int = 0) -> str:
+    if not _have_device():
+        return "cuda/hip device unavailable"
+    try:
+        return torch.cuda.get_device_name(index)
+    except Exception as exc:
+        return f"device name unavailable: {type(exc).__name__}: {exc}"
+
+
 def detect_runtime() -> dict[str, Any]:
-    torch, torch_error = _torch()
-    info: dict[str, Any] = {
-        "torch_imported": torch is not None,
-        "torch_error": torch_error,
-        "torch_version": getattr(torch, "__version__", None) if torch is not None else None,
-        "torch_version_hip": getattr(getattr(torch, "version", None), "hip", None) if torch is not None else None,
-        "torch_cuda_is_available": _cuda_available(torch) if torch is not None else False,
-        "device": get_device_name(),
-        "gfx_target": best_effort_gfx_target(),
-        "is_rocm_pytorch": is_rocm_pytorch(),
-    }
-    info["is_mi355x"] = info["gfx_target"] == TARGET
+    """The facts the gate and the loader use, as one dict."""
+    available = _have_device()
+    target = device_gfx_target(0) if available else None
     loaded, detail = native_status()
-    info["native_available"] = loaded
-    info["native_info"] = detail
-    return info
+    return {
+        "torch_imported": True,
+        "torch_error": None,
+        "torch_version": torch.__version__,
+        "torch_version_hip": torch.version.hip,
+        "torch_cuda_is_available": available,
+        "device": get_device_name(),
+        "gfx_target": target,
+        "is_rocm_pytorch": is_rocm_pytorch(),
+        "is_mi355x": target == TARGET,
+        "native_available": loaded,
+        "native_info": detail,
+    }
 
 
 def explain_dispatch(info: dict[str, Any] | None = None) -> str:
+    """Text report of detect_runtime(), plus the diagnostics dict of a dispatch when given."""
     runtime = detect_runtime()
-    lines = [
-        "MI355X attention dispatch diagnostics",
-        f"torch: {runtime['torch_version']} imported={runtime['torch_imported']}",
-        f"torch.version.hip: {runtime['torch_version_hip']}",
-        f"torch.cuda.is_available: {runtime['torch_cuda_is_available']}",
-        f"device: {runtime['device']}",
-        f"gfx target: {runtime['gfx_target']}",
-        f"MI355X (gfx950) target: {runtime['is_mi355x']}",
-        f"HIP library: {runtime['native_available']} ({runtime['native_info']})",
-    ]
+    labels = (("torch", "torch_version"), ("torch.version.hip", "torch_version_hip"),
+              ("torch.cuda.is_available", "torch_cuda_is_available"), ("device", "device"),
+              ("gfx target", "gfx_target"), (f"MI355X ({TARGET}) target", "is_mi355x"))
+    lines = ["MI355X attention dispatch diagnostics"]
+    lines += [f"{label}: {runtime[key]}" for label, key in labels]
+    lines.append(f"HIP library: {runtime['native_available']} ({runtime['native_info']})")
     if info:
         lines.append("last dispatch:")
-        lines.extend(f"  {key}: {info[key]}" for key in sorted(info))
+        lines += [f"  {key}: {info[key]}" for key in sorted(info)]
     return "\n".join(lines)
