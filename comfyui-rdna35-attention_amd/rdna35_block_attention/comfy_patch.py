@@ -16,14 +16,9 @@ import torch
 
 from .diagnostics import NativeUnavailableError
 from .dispatch import fixed_block_attention
+from .gates import chain as _fallback_call
 
 LOG_PREFIX = "MI355X FixedBlockAttention"
-
-
-def _fallback_call(previous_override: Callable | None, original_func: Callable, *args, **kwargs):
-    if previous_override is not None:
-        return previous_override(original_func, *args, **kwargs)
-    return original_func(*args, **kwargs)
 
 
 def _options(kwargs: dict[str, Any]) -> dict:
