@@ -465,6 +465,63 @@ int pisa_hip_attend(int32_t dtype, int32_t batch, int32_t heads, int32_t tokens,
                        batch * heads, static_cast<hipStream_t>(stream));
 }
 
+// ---- allocation-free forward (pisa_hip_forward_noalloc) -----------------
+// Callers that cannot allocate (code under HIP graph capture, tight serving
+// loops, hosts that forbid hipMalloc) run the PISA forward in this file-scope
+// device array instead of a caller workspace.  Every GPU the library runs on
+// holds its own copy (PISA_NOALLOC_SCRATCH_BYTES) until the process ends.  Its
+// device address is looked up once per device with hipGetSymbolAddress; host
+// code never uses the array's name as an address (on the host it is only a
+// stand-in for the symbol).
+static __device__ __align__(256) unsigned char scratch[PISA_NOALLOC_SCRATCH_BYTES];
+
+}  // extern "C"
+
+namespace pisa_host {
+
+static int scratch_address(void** out) {
+    static std::mutex mu;
+    static void* per_device[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return fail(PISA_ERR_DEVICE, "hipGetDevice failed");
+    if (dev < 0 || dev >= 64) return fail(PISA_ERR_DEVICE, "device index %d out of range", dev);
+    std::lock_guard<std::mutex> lock(mu);
+    if (!per_device[dev]) {
+        void* ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr)
+            return fail(PISA_ERR_DEVICE, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                        hipGetErrorString(e));
+        per_device[dev] = ptr;
+    }
+    *out = per_device[dev];
+    return PISA_OK;
+}
+
+}  // namespace pisa_host
+
+extern "C" {
+
+int pisa_hip_forward_noalloc(int32_t dtype, int32_t batch, int32_t heads, int32_t tokens, int32_t head_dim,
+                             pisa_view q, pisa_view k, pisa_view v, pisa_view out, pisa_token_grid grid,
+                             int32_t exact_blocks, float scale, int32_t sink_block, int32_t stats_mode,
+                             int32_t route_mode, int32_t first_order, void* stream) {
+    // the size check comes first, so an oversized problem never touches the device
+    const int64_t need = pisa_hip_forward_workspace_bytes(batch, heads, tokens, head_dim, exact_blocks);
+    if (need > PISA_NOALLOC_SCRATCH_BYTES)
+        return fail(PISA_ERR_WORKSPACE,
+                    "pisa_hip_forward_noalloc: this problem needs %lld bytes of scratch, the static scratch holds %lld "
+                    "(use pisa_hip_forward with a caller workspace)",
+                    (long long)need, (long long)PISA_NOALLOC_SCRATCH_BYTES);
+    if (!valid_dtype(dtype)) return fail(PISA_ERR_UNSUPPORTED, "PISA forward supports bf16 and fp16 only");
+    void* ws = nullptr;
+    int rc;
+    if ((rc = check_device()) || (rc = scratch_address(&ws))) return rc;
+    return pisa_hip_forward(dtype, batch, heads, tokens, head_dim, q, k, v, out, grid, exact_blocks, scale,
+                            sink_block, stats_mode, route_mode, first_order, nullptr, nullptr, ws,
+                            PISA_NOALLOC_SCRATCH_BYTES, stream);
+}
+
 int64_t pisa_hip_block_stats_workspace_bytes(int32_t batch, int32_t heads, int32_t tokens, int32_t head_dim) {
     if (batch <= 0 || heads <= 0 || tokens <= 0 || head_dim <= 0) return 0;
     const StatsPlan p = plan_stats(batch * heads, tokens);

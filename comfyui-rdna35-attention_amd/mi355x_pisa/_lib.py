@@ -75,6 +75,11 @@ _SIGNATURES = {
         [_i32, _i32, _i32, _i32, _i32, PisaView, PisaView, PisaView, PisaView, PisaTokenGrid,
          _i32, _f32, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _i64, _vp],
     ),
+    "pisa_hip_forward_noalloc": (
+        ctypes.c_int,
+        [_i32, _i32, _i32, _i32, _i32, PisaView, PisaView, PisaView, PisaView, PisaTokenGrid,
+         _i32, _f32, _i32, _i32, _i32, _i32, _vp],
+    ),
     "pisa_hip_prepare": (
         ctypes.c_int,
         [_i32, _i32, _i32, _i32, _i32, PisaView, PisaView, PisaView, PisaView, PisaTokenGrid,

@@ -194,6 +194,28 @@ PISA_HIP_EXPORT int pisa_hip_attend(int32_t dtype, int32_t batch, int32_t heads,
                     int32_t stats_mode, int32_t route_mode, int32_t first_order,
                     void* workspace, int64_t workspace_bytes, void* stream);
 
+/*
+ * pisa_hip_forward without a caller workspace and without any allocation.
+ * This entry point has no counterpart in the reference: it exists for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, hosts that forbid hipMalloc).  The workspace is a static
+ * device array of PISA_NOALLOC_SCRATCH_BYTES (256 MiB) inside the library,
+ * one per GPU, held until the process ends; a problem whose
+ * pisa_hip_forward_workspace_bytes exceeds it is refused with
+ * PISA_ERR_WORKSPACE before anything is launched (the Anima profile
+ * B=2 H=16 T=9216 needs 197 MB).  No debug outputs.  Every call on one GPU
+ * uses that GPU's one array: calls that overlap on one GPU (two streams, two
+ * host threads) race and must be serialised by the caller; calls in one
+ * stream are ordered and safe.  Nothing in the array needs to start at zero
+ * (every stage writes what it later reads), so no clearing is enqueued.
+ * Arguments as pisa_hip_forward.
+ */
+#define PISA_NOALLOC_SCRATCH_BYTES (256LL << 20)
+PISA_HIP_EXPORT int pisa_hip_forward_noalloc(int32_t dtype, int32_t batch, int32_t heads, int32_t tokens,
+                             int32_t head_dim, pisa_view q, pisa_view k, pisa_view v, pisa_view out,
+                             pisa_token_grid grid, int32_t exact_blocks, float scale, int32_t sink_block,
+                             int32_t stats_mode, int32_t route_mode, int32_t first_order, void* stream);
+
 /* ---- subsystem 1: block statistics ------------------------------------- */
 
 PISA_HIP_EXPORT int64_t pisa_hip_block_stats_workspace_bytes(int32_t batch, int32_t heads, int32_t tokens,
