@@ -28,7 +28,7 @@ def dense_attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float | 
 
 def fixed_block_attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, block_size: int = 64,
                           scale: float | None = None, causal: bool = False, out_dtype: str = "f32",
-                          mask: np.ndarray | None = None) -> np.ndarray:
+                          mask: np.ndarray | None = None, prob_dtype: str | None = None) -> np.ndarray:
     """Block loop of fixed_block_attention_ref (reference.py:159-200) on [..., T, D] arrays.
 
     Each block of block_size tokens attends only to itself (the last block
@@ -38,6 +38,8 @@ def fixed_block_attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, block_siz
     (-inf elsewhere), any other dtype is added to the scaled score.  A row
     with every score -inf gives NaN, the value torch.softmax returns.
     Scores, softmax and P@V in float64; output rounded to out_dtype.
+    prob_dtype rounds the normalised probabilities before P@V: the Triton
+    kernel's `probs.to(v.dtype)` (triton_kernel.py:92-96), used for fp16/bf16.
     """
     q64 = np.asarray(q, dtype=np.float64)
     k64 = np.asarray(k, dtype=np.float64)
@@ -60,6 +62,8 @@ def fixed_block_attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, block_siz
         p, _ = softmax_lse(scores)
         dead = np.all(np.isneginf(scores), axis=-1, keepdims=True)
         p = np.where(dead, np.nan, p)
+        if prob_dtype is not None:
+            p = round_dtype(p, prob_dtype).astype(np.float64)
         out[..., start:end, :] = np.matmul(p, v64[..., start:end, :])
     return round_dtype(out, out_dtype)
 

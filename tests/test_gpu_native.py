@@ -405,10 +405,33 @@ def test_h3_strided_views_equal_packed_copies(native):
 @pytest.mark.parametrize("tokens", [64, 65, 200])
 @pytest.mark.parametrize("causal", [False, True])
 def test_fixed_block_matches_oracle(native, dtype, head_dim, tokens, causal):
+    """fp16/bf16 run the matrix-core kernel with the Triton kernel's rounding of the normalised
+    probabilities to the input dtype (triton_kernel.py:92-96); fp32 the fp32 kernel."""
     gen = torch.Generator().manual_seed(tokens + head_dim)
     q, k, v = (torch.randn((1, 2, tokens, head_dim), generator=gen).to(dtype).cuda() for _ in range(3))
     out = native.fixed_block_attention(q, k, v, 1 / math.sqrt(head_dim), causal)
     name = {torch.float32: "f32", torch.float16: "f16", torch.bfloat16: "bf16"}[dtype]
-    expected = oatt.fixed_block_attention(np32(q), np32(k), np32(v), causal=causal, out_dtype=name)
+    prob = None if dtype == torch.float32 else name
+    expected = oatt.fixed_block_attention(np32(q), np32(k), np32(v), causal=causal, out_dtype=name, prob_dtype=prob)
     tol = {torch.float32: 1e-5, torch.float16: 2e-3, torch.bfloat16: 1e-2}[dtype]
     assert_close(np32(out), expected, tol, tol, "fixed block")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_fixed_block_16bit_paths_on_large_and_unaligned_inputs(native, dtype):
+    """Many blocks through the matrix-core kernel (B=2 H=16 T=4096 D=128, a ComfyUI-sized call),
+    and rows whose stride is not a multiple of 8 elements, which take the fp32 kernel instead."""
+    gen = torch.Generator().manual_seed(41)
+    name = {torch.float16: "f16", torch.bfloat16: "bf16"}[dtype]
+    tol = {torch.float16: 2e-3, torch.bfloat16: 1e-2}[dtype]
+    q, k, v = (torch.randn((2, 16, 4096, 128), generator=gen).to(dtype).cuda() for _ in range(3))
+    out = native.fixed_block_attention(q, k, v, 128 ** -0.5, True)
+    for b, h in ((0, 0), (1, 15)):
+        expected = oatt.fixed_block_attention(np32(q[b, h]), np32(k[b, h]), np32(v[b, h]), causal=True,
+                                              out_dtype=name, prob_dtype=name)
+        assert_close(np32(out[b, h]), expected, tol, tol, f"fixed block head {(b, h)}")
+    wide = [torch.randn((1, 2, 130, 68), generator=gen).to(dtype).cuda() for _ in range(3)]
+    qs, ks, vs = (t[..., :64] for t in wide)  # token stride 68: not 16-byte aligned rows
+    out = native.fixed_block_attention(qs, ks, vs, 0.125, False)
+    expected = oatt.fixed_block_attention(np32(qs), np32(ks), np32(vs), scale=0.125, out_dtype=name)
+    assert_close(np32(out), expected, tol, tol, "fixed block unaligned")
