@@ -119,3 +119,14 @@ def test_other_entry_points_validate(lib):
     misaligned = lib.PisaView(0x1002, 0, 0, 128)
     assert lib.LIB.pisa_hip_pack_spatial_qkv(0, 1, 1, 9216, 128, misaligned, k, v, lib.grid(1, 96, 96), None,
                                              None, None, None) == 1
+
+
+def test_reference_module_name_is_the_implementation():
+    """`import rdna35_pisa_ck` (the reference's native package name) yields the mi355x_pisa module."""
+    import mi355x_pisa
+    import rdna35_pisa_ck
+
+    assert rdna35_pisa_ck is mi355x_pisa
+    assert rdna35_pisa_ck.forward_spatial_bhtd is mi355x_pisa.forward_spatial_bhtd
+    assert rdna35_pisa_ck.capabilities()["architecture"] == "gfx950"
+    assert rdna35_pisa_ck.SPATIAL_SPARSE_EXACT_BLOCKS == 23
