@@ -252,9 +252,24 @@ def run_workload(name: str, args) -> dict:
         roof = {"bound": "hbm", "kernel": "fixed_block_kernel", "achieved": round(achieved / 1e9, 1),
                 "peak": PEAK_HBM_BYTES / 1e9, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_BYTES, 4),
                 "traffic": None}
+        # the HBM floor at this size: one device copy that reads and writes the same 33.5 MB
+        src = torch.empty(2 * math.prod(shape), dtype=torch.float32, device=device).fill_(1.0)
+        dst = torch.empty_like(src)
+        copy_ms = time_gpu(lambda: dst.copy_(src), args.steps, args.warmup)
+        # the matrix-core path of bf16 inputs (the reference's Triton kernel), at C1's shape and at C4's
+        mfma = {}
+        for label, mshape in (("c1_shape", shape), ("anima_shape", (2, 16, 9216, 128))):
+            mq, mk, mv = (randn(mshape, torch.bfloat16) for _ in range(3))
+            mms = time_gpu(lambda: mi355x_pisa.fixed_block_attention(mq, mk, mv, mshape[-1] ** -0.5), args.steps,
+                           args.warmup)
+            mbytes = 4 * math.prod(mshape) * 2
+            mfma[label] = {"shape": list(mshape), "ms": round(mms, 4), "GB/s": round(mbytes / (mms * 1e-3) / 1e9, 1),
+                           "hbm_frac": round(mbytes / (mms * 1e-3) / PEAK_HBM_BYTES, 4)}
+            del mq, mk, mv
         result = _line("C1 fixed block-diagonal attention ms, fp32 B=1 H=8 T=4096 D=64", ms, args,
                        {"workload": "fixed_block_diagonal", "batch": 1, "heads": 8, "tokens": 4096, "head_dim": 64,
-                        "block": 64}, roof, dtype="f32")
+                        "block": 64}, roof, dtype="f32",
+                       extra={"same_bytes_copy_ms": round(copy_ms, 4), "bf16_mfma_kernel": mfma})
         if not args.no_cpu_baseline:
             blocks = [t.detach().cpu().reshape(1, 8, 64, 64, 64) for t in (q, k, v)]
 
@@ -273,12 +288,16 @@ def run_workload(name: str, args) -> dict:
         v = randn((2, 16, kv_tokens, 128), torch.bfloat16, 0.5)
         s = 1 / math.sqrt(128)
         ms = time_gpu(lambda: mi355x_pisa.dense_attention(q, k, v, s), args.steps, args.warmup)
+        sdpa_ms = time_gpu(lambda: torch.nn.functional.scaled_dot_product_attention(q, k, v, scale=s),
+                           max(2, args.steps // 4), 2)
         flops = 4.0 * 32 * 9216 * kv_tokens * 128
         label = "self" if name == "c2" else "cross Tk=512"
         result = _line(f"C2 exact full attention ms ({label}), bf16 B=2 H=16 Tq=9216 Tk={kv_tokens} D=128", ms, args,
                        {"workload": "dense_exact_attention", "batch": 2, "heads": 16, "q_tokens": 9216,
                         "kv_tokens": kv_tokens, "head_dim": 128},
                        _mfma_roofline("kv_pack_kernel + attention_persistent_kernel (dense)", flops, ms),
+                       extra={"torch_sdpa_ms": round(sdpa_ms, 4),
+                              "torch_sdpa_tflops": round(flops / (sdpa_ms * 1e-3) / 1e12, 2)},
                        data="synthetic: seeded 0.5*N(0,1)")
         if not args.no_cpu_baseline:
             rows = 2048 if name == "c2" else 9216
