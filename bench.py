@@ -76,6 +76,7 @@ BASELINE_MS = 25.121  # the reference's published C4 call time, measured on gfx1
 METRIC = "PISA call ms + MFMA util %, bf16 B=2 H=16 T=9216 D=128, 23/144 blocks"
 COPY_BYTES = 1 << 30          # profile run: elementwise copy of 1 GiB (reads and writes COPY_BYTES)
 PROFILE_ATTENDS = 40
+GRAPH_CALLS = 20              # C1: calls captured in one HIP graph to time the kernel without host gaps
 TRAFFIC_FILE = REPO / "profiles" / "attention_c4_traffic.json"
 
 
@@ -110,6 +111,41 @@ def time_gpu(fn, steps: int, warmup: int) -> float:
     end.record()
     torch.cuda.synchronize()
     return start.elapsed_time(end) / steps
+
+
+def time_graph(fn, calls: int, replays: int, warmup: int) -> float:
+    """Mean ms per call of `fn` captured `calls` times in one HIP graph, over `replays` replays.
+
+    The graph is replayed `warmup` times first and its last output is compared
+    with an eager call of `fn` (every captured call computes the same result).
+    """
+    import torch
+
+    eager = fn()
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):  # first calls outside the capture (lazy initialisation)
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(calls):
+            out = fn()
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    if not torch.equal(out, eager):
+        raise RuntimeError("graph replay differs from the eager call")
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(replays):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / (replays * calls)
 
 
 def cpu_threads() -> int:
@@ -246,12 +282,17 @@ def run_workload(name: str, args) -> dict:
     if name == "c1":
         shape = (1, 8, 4096, 64)
         q, k, v = (randn(shape, torch.float32) for _ in range(3))
-        ms = time_gpu(lambda: mi355x_pisa.fixed_block_attention(q, k, v, 0.125), args.steps, args.warmup)
+        call = lambda: mi355x_pisa.fixed_block_attention(q, k, v, 0.125)  # noqa: E731
+        ms = time_gpu(call, args.steps, args.warmup)
+        # the eager call of this 33.5 MB problem is bound by its host path (argument checks, ctypes
+        # marshalling, launch); the kernel's own rate is timed on GRAPH_CALLS calls captured in one
+        # HIP graph, replayed back to back (no host work between launches)
+        kernel_ms = time_graph(call, GRAPH_CALLS, max(1, args.steps // GRAPH_CALLS), 2)
         nbytes = 4 * math.prod(shape) * 4
-        achieved = nbytes / (ms * 1e-3)
-        roof = {"bound": "hbm", "kernel": "fixed_block_kernel", "achieved": round(achieved / 1e9, 1),
+        achieved = nbytes / (kernel_ms * 1e-3)
+        roof = {"bound": "hbm", "kernel": "fixed_block_f32_mfma_kernel", "achieved": round(achieved / 1e9, 1),
                 "peak": PEAK_HBM_BYTES / 1e9, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_BYTES, 4),
-                "traffic": None}
+                "traffic": None, "timed": f"{GRAPH_CALLS} calls per HIP graph replay"}
         # the HBM floor at this size: one device copy that reads and writes the same 33.5 MB
         src = torch.empty(2 * math.prod(shape), dtype=torch.float32, device=device).fill_(1.0)
         dst = torch.empty_like(src)
@@ -269,7 +310,8 @@ def run_workload(name: str, args) -> dict:
         result = _line("C1 fixed block-diagonal attention ms, fp32 B=1 H=8 T=4096 D=64", ms, args,
                        {"workload": "fixed_block_diagonal", "batch": 1, "heads": 8, "tokens": 4096, "head_dim": 64,
                         "block": 64}, roof, dtype="f32",
-                       extra={"same_bytes_copy_ms": round(copy_ms, 4), "bf16_mfma_kernel": mfma})
+                       extra={"kernel_ms_graph": round(kernel_ms, 4), "same_bytes_copy_ms": round(copy_ms, 4),
+                              "bf16_mfma_kernel": mfma})
         if not args.no_cpu_baseline:
             blocks = [t.detach().cpu().reshape(1, 8, 64, 64, 64) for t in (q, k, v)]
 

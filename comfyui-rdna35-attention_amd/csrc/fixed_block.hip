@@ -1,9 +1,10 @@
 // Fixed block-diagonal attention: every 64-token block attends only to itself.
 //
-// Two kernels.  bf16/fp16 calls without a mask run fixed_block_mfma_kernel
-// (matrix cores, the reference's Triton semantics, below).  fp32 calls and
-// masked calls - the ones the reference sends to its eager fp32 loop - run
-// fixed_block_kernel:
+// Three kernels.  bf16/fp16 calls without a mask run fixed_block_mfma_kernel
+// (matrix cores, the reference's Triton semantics, below); fp32 calls without
+// a mask run fixed_block_f32_mfma_kernel (fp32 matrix cores, below).  Masked
+// calls and rows that are not 16-byte aligned - the calls the reference sends
+// to its eager fp32 loop - run fixed_block_kernel:
 //
 // One 256-thread workgroup per (block, batch*head).  The block's Q, K and V
 // (64 x D) are staged in LDS as fp32; thread (rt, kt) = (t/16, t%16) owns the
@@ -166,57 +167,50 @@ __global__ __launch_bounds__(256) void fixed_block_kernel(View q, View k, View v
 // semantics of the reference's Triton kernel (triton_kernel.py:53-100): scores
 // with fp32 accumulation, softmax in fp32, probabilities normalised and then
 // rounded to the input dtype, P @ V with fp32 accumulation, rounded output.
-// The block is staged in LDS - Q and K row-major, V transposed with its key
-// index in swap23 order - and the products are formed transposed as in the
-// attention kernels (S^T = K Q^T, O^T = V^T P^T), so a query is a lane column
-// and the probabilities feed the second MFMA from their accumulator registers.
+//
+// Nothing is staged in LDS, so the occupancy is set by registers alone.  The
+// products are formed transposed as in the attention kernels (S^T = K Q^T,
+// O^T = V^T P^T): a query is a lane column and the probabilities feed the
+// second MFMA from their accumulator registers.  The Q and K operands are 16
+// bytes of one row per lane (rows 32x + col, dims 16t + 8half .. +7), read
+// straight from the rows.  The V^T operand needs 8 keys of one dim per lane;
+// the dims of an output tile are assigned so that a lane reads MD = D/32
+// consecutive dims of a key row with one load (output tile md holds dims
+// MD*i + md of accumulator row i), one load instruction covers two whole key
+// rows, and the operand of tile md takes element md of 8 such loads.
 template <typename T, int D>
 __global__ __launch_bounds__(64) void fixed_block_mfma_kernel(View q, View k, View v, OutView o, int tokens,
                                                                int nblocks, float scale_log2, int causal) {
     typedef typename Elem<T>::vec8 vec8;
-    constexpr int KT = D / 16;      // 16-deep k-steps of the score product
-    constexpr int MD = D / 32;      // 32-dim tiles of the output
-    constexpr int P = D / 8;        // 16-byte pieces per row
-    constexpr int kRow = D + 8;     // padded row (elements) of the row-major Q and K tiles
-    constexpr int kVtRow = 64 + 8;  // padded row (elements) of the transposed V tile
-    __shared__ __attribute__((aligned(16))) T q_lds[64 * kRow];
-    __shared__ __attribute__((aligned(16))) T k_lds[64 * kRow];
-    __shared__ __attribute__((aligned(16))) T vt_lds[D * kVtRow];
+    constexpr int KT = D / 16;  // 16-deep k-steps of the score product
+    constexpr int MD = D / 32;  // output dim tiles; dims a lane reads per key row
+    typedef T vecmd __attribute__((ext_vector_type(MD)));
     const int lane = threadIdx.x;
     const int half = lane >> 5;
     const int col = lane & 31;
     const int bh = blockIdx.x / nblocks;
     const int start = (blockIdx.x - bh * nblocks) * 64;
     const int len = min(64, tokens - start);
-
-    // ---- stage: piece id = row * P + pc (rows past len are zero)
-    for (int id = lane; id < 64 * P; id += 64) {
-        const int r = id / P;
-        const int pc = id - r * P;
-        const int tok = start + min(r, len - 1);
-        vec8 xq = load8<vec8>(q.data + (q.row(bh, tok) + pc * 8) * (int64_t)sizeof(T));
-        vec8 xk = load8<vec8>(k.data + (k.row(bh, tok) + pc * 8) * (int64_t)sizeof(T));
-        vec8 xv = load8<vec8>(v.data + (v.row(bh, tok) + pc * 8) * (int64_t)sizeof(T));
-        if (r >= len) {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                xq[e] = T(0.0f);
-                xk[e] = T(0.0f);
-                xv[e] = T(0.0f);
-            }
-        }
-        store8(&q_lds[r * kRow + pc * 8], xq);
-        store8(&k_lds[r * kRow + pc * 8], xk);
-        const int pos = swap23(r);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {  // rotated by the piece, so the 16 lanes of a row hit 16 banks
-            const int ee = (e + pc) & 7;
-            vt_lds[(pc * 8 + ee) * kVtRow + pos] = xv[ee];
-        }
-    }
-    __syncthreads();
+    auto at = [&](const View& x, int r) {  // row r of the block, clamped to the last real row
+        return x.data + x.row(bh, start + min(r, len - 1)) * (int64_t)sizeof(T);
+    };
 
     // ---- S^T[key][query] for key tiles mt and query tiles nt
+    // requested k-step by k-step, the order the products consume them
+    vec8 kf[2][KT], qf[2][KT];
+    const char* krow[2] = {at(k, col), at(k, 32 + col)};
+    const char* qrow[2] = {at(q, col), at(q, 32 + col)};
+#pragma unroll
+    for (int t = 0; t < KT; ++t)
+#pragma unroll
+        for (int x = 0; x < 2; ++x) {
+            kf[x][t] = load8<vec8>(krow[x] + (16 * t + 8 * half) * sizeof(T));
+            qf[x][t] = load8<vec8>(qrow[x] + (16 * t + 8 * half) * sizeof(T));
+        }
+    // every Q and K request is issued before the first product (the
+    // scheduler would otherwise issue each just before its use, one memory
+    // round trip at a time), and the V requests right after the products
+    __builtin_amdgcn_sched_barrier(0);
     f32x16 s[2][2];
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
@@ -225,22 +219,33 @@ __global__ __launch_bounds__(64) void fixed_block_mfma_kernel(View q, View k, Vi
 #pragma unroll
             for (int e = 0; e < 16; ++e) s[mt][nt][e] = 0.0f;
 #pragma unroll
-    for (int t = 0; t < KT; ++t) {
-        vec8 kf[2], qf[2];
-#pragma unroll
-        for (int x = 0; x < 2; ++x) {
-            kf[x] = *reinterpret_cast<const vec8*>(&k_lds[(32 * x + col) * kRow + 16 * t + 8 * half]);
-            qf[x] = *reinterpret_cast<const vec8*>(&q_lds[(32 * x + col) * kRow + 16 * t + 8 * half]);
-        }
+    for (int t = 0; t < KT; ++t)
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-            for (int nt = 0; nt < 2; ++nt) s[mt][nt] = mfma32(kf[mt], qf[nt], s[mt][nt]);
-    }
+            for (int nt = 0; nt < 2; ++nt) s[mt][nt] = mfma32(kf[mt][t], qf[nt][t], s[mt][nt]);
+
+    // ---- value rows: key 32mt + 16ss + 4half + 8(e/4) + e%4 (the key of
+    // probability element e of k-step (mt, ss) in this lane), dims MD*col ..
+    // Keys past the block's length read its last row and get probability 0.
+    // The loads are unconditional: behind a branch, the compiler's wait
+    // counts would wait for every earlier load before each of them.
+    vecmd vr[2][2][8];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int ss = 0; ss < 2; ++ss)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int key = 32 * mt + 16 * ss + 4 * half + 8 * (e >> 2) + (e & 3);
+                vr[mt][ss][e] = *reinterpret_cast<const vecmd*>(at(v, key) + MD * col * sizeof(T));
+            }
+
+    __builtin_amdgcn_sched_barrier(0);
 
     // ---- masking and the softmax of query column (nt, col), in log2 units:
-    // accumulator v of tile mt is key 32mt + 8(v/4) + 4half + v%4
-    typename Elem<T>::vec8 pf[2][2][2];  // [nt][mt][ss]: 8 probabilities, keys 16ss.. of tile mt in swap23 order
+    // accumulator e of tile mt is key 32mt + 8(e/4) + 4half + e%4
+    vec8 pf[2][2][2];  // [nt][mt][ss]: 8 probabilities, elements 8ss .. 8ss+7 of tile mt
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
         const int query = 32 * nt + col;
@@ -274,7 +279,7 @@ __global__ __launch_bounds__(64) void fixed_block_mfma_kernel(View q, View k, Vi
                 for (int e = 0; e < 8; ++e) pf[nt][mt][ss][e] = from_f32<T>(s[mt][nt][ss * 8 + e] * inv);
     }
 
-    // ---- O^T[dim][query] = sum_key V^T[dim][key] P^T[key][query]
+    // ---- O^T[dim][query] = sum_key V^T[dim][key] P^T[key][query]; row i of tile md is dim MD*i + md
     f32x16 acc[MD][2];
 #pragma unroll
     for (int md = 0; md < MD; ++md)
@@ -283,33 +288,169 @@ __global__ __launch_bounds__(64) void fixed_block_mfma_kernel(View q, View k, Vi
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[md][nt][e] = 0.0f;
 #pragma unroll
-    for (int md = 0; md < MD; ++md)
+    for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
+        for (int ss = 0; ss < 2; ++ss)
 #pragma unroll
-            for (int ss = 0; ss < 2; ++ss) {
-                const vec8 vf = *reinterpret_cast<const vec8*>(
-                    &vt_lds[(32 * md + col) * kVtRow + 32 * mt + 16 * ss + 8 * half]);
+            for (int md = 0; md < MD; ++md) {
+                vec8 vf;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) vf[e] = vr[mt][ss][e][md];
 #pragma unroll
                 for (int nt = 0; nt < 2; ++nt) acc[md][nt] = mfma32(vf, pf[nt][mt][ss], acc[md][nt]);
             }
 
-    // ---- store: accumulator v of tile md is dim 32md + 8(v/4) + 4half + v%4 of query 32nt + col
-    typedef T vec4 __attribute__((ext_vector_type(4)));
+    // ---- store: accumulator e of every tile is row i = 8(e/4) + 4half + e%4,
+    // i.e. dims MD*i .. MD*i + MD-1 of query 32nt + col across the MD tiles
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
         const int query = 32 * nt + col;
         if (query >= len) continue;
         char* dst = o.data + o.row(bh, start + query) * (int64_t)sizeof(T);
 #pragma unroll
-        for (int md = 0; md < MD; ++md)
+        for (int e = 0; e < 16; ++e) {
+            const int i = 8 * (e >> 2) + 4 * half + (e & 3);
+            vecmd x;
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                vec4 x;
+            for (int md = 0; md < MD; ++md) x[md] = from_f32<T>(acc[md][nt][e]);
+            *reinterpret_cast<vecmd*>(dst + MD * i * sizeof(T)) = x;
+        }
+    }
+}
+
+// fp32 without a mask: four waves per block on v_mfma_f32_16x16x4_f32 (fp32
+// operands, fp32 accumulation), the arithmetic of fixed_block_kernel above
+// (fp32 scores, softmax with expf, fp32 P @ V).  Wave w owns queries
+// 16w .. 16w+15 (a lane column c = lane % 16, lane group g = lane / 16).
+//   S^T = K Q^T: k-step t = 4s + e contracts dim 16s + 4g + e in lane group g,
+//     so each lane reads its K and Q rows as float4 pieces (dims 16s + 4g ..);
+//     accumulator r of key tile n is key 16n + 4g + r of query 16w + c.
+//   O^T = V^T P^T: k-step (n, r) contracts key 16n + 4g + r, exactly the
+//     probability the lane holds in accumulator r of key tile n.  Row i of
+//     output tile m is dim VW*i + m (VW = D/16), so a lane reads VW
+//     consecutive dims of a key row with one load and, at the end, holds the
+//     4*VW consecutive dims 4*VW*g .. of its query.
+// Nothing is staged in LDS; rows past the block's length are read clamped to
+// its last row (unconditional loads, so the compiler's wait counts stay
+// partial) and get probability 0 (keys) or are not stored (queries).
+template <int D>
+__global__ __launch_bounds__(256) void fixed_block_f32_mfma_kernel(View q, View k, View v, OutView o, int tokens,
+                                                                   int nblocks, float scale, int causal) {
+    constexpr int S4 = D / 16;  // float4 pieces of a Q or K row per lane
+    constexpr int VW = D / 16;  // V dims per lane per key row = output dim tiles
+    const int lane = threadIdx.x & 63;
+    const int w = threadIdx.x >> 6;
+    const int c = lane & 15;
+    const int g = lane >> 4;
+    const int bh = blockIdx.x / nblocks;
+    const int start = (blockIdx.x - bh * nblocks) * 64;
+    const int len = min(64, tokens - start);
+    auto at = [&](const View& x, int r) {
+        return reinterpret_cast<const float*>(x.data) + x.row(bh, start + min(r, len - 1));
+    };
+
+    f32x4 qv[S4], kv[4][S4];
+    {
+        const float* qr = at(q, 16 * w + c);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) x[e] = from_f32<T>(acc[md][nt][4 * g + e]);
-                *reinterpret_cast<vec4*>(dst + (32 * md + 8 * g + 4 * half) * sizeof(T)) = x;
+        for (int s4 = 0; s4 < S4; ++s4) qv[s4] = *reinterpret_cast<const f32x4*>(qr + 16 * s4 + 4 * g);
+    }
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+        const float* kr = at(k, 16 * n + c);
+#pragma unroll
+        for (int s4 = 0; s4 < S4; ++s4) kv[n][s4] = *reinterpret_cast<const f32x4*>(kr + 16 * s4 + 4 * g);
+    }
+    float vv[4][4][VW];
+#pragma unroll
+    for (int n = 0; n < 4; ++n)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int key = 16 * n + 4 * g + r;
+            const float* vr = at(v, key) + VW * c;
+            if constexpr (VW == 2) {
+                const float2 x = *reinterpret_cast<const float2*>(vr);
+                vv[n][r][0] = x.x;
+                vv[n][r][1] = x.y;
+            } else {
+#pragma unroll
+                for (int j = 0; j < VW; j += 4) {
+                    const f32x4 x = *reinterpret_cast<const f32x4*>(vr + j);
+#pragma unroll
+                    for (int jj = 0; jj < 4; ++jj) vv[n][r][j + jj] = x[jj];
+                }
             }
+        }
+
+    // all requests before the first product at D <= 64 (at D = 128 the rows
+    // held at once would cost occupancy)
+    if constexpr (D <= 64) __builtin_amdgcn_sched_barrier(0);
+    // key tile by key tile, in the order the rows were requested: the products
+    // of a tile wait only for its own rows (every block of the grid loads at
+    // once, so the rows arrive over the whole HBM transfer)
+    f32x4 sacc[4];
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+        sacc[n] = f32x4(0.0f);
+#pragma unroll
+        for (int s4 = 0; s4 < S4; ++s4)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                sacc[n] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[n][s4][e], qv[s4][e], sacc[n], 0, 0, 0);
+    }
+
+    // softmax of query column 16w + c: its 64 keys are 16 accumulators in each of the lanes c, c+16, c+32, c+48
+    const int query = 16 * w + c;
+    float mx = -__builtin_inff();
+#pragma unroll
+    for (int n = 0; n < 4; ++n)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int key = 16 * n + 4 * g + r;
+            const bool dead = key >= len || (causal && key > query);
+            sacc[n][r] = dead ? -__builtin_inff() : sacc[n][r] * scale;
+            mx = fmaxf(mx, sacc[n][r]);
+        }
+    {
+        const float2 p16 = pair_xor16(mx);
+        mx = max_xor32(fmaxf(p16.x, p16.y));
+    }
+    const float m_use = (mx == -__builtin_inff()) ? 0.0f : mx;
+    float sum = 0.0f;
+#pragma unroll
+    for (int n = 0; n < 4; ++n)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            sacc[n][r] = expf(sacc[n][r] - m_use);
+            sum += sacc[n][r];
+        }
+    sum = add_xor32(add_xor16(sum));
+    const float inv = sum > 0.0f ? 1.0f / sum : __builtin_nanf("");  // all keys masked
+#pragma unroll
+    for (int n = 0; n < 4; ++n)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sacc[n][r] *= inv;
+
+    f32x4 oacc[VW];
+#pragma unroll
+    for (int m = 0; m < VW; ++m) oacc[m] = f32x4(0.0f);
+#pragma unroll
+    for (int n = 0; n < 4; ++n)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int m = 0; m < VW; ++m)
+                oacc[m] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[n][r][m], sacc[n][r], oacc[m], 0, 0, 0);
+
+    if (query >= len) return;
+    // dims 4*VW*g + VW*r + m hold oacc[m][r]: 4*VW consecutive floats
+    float* dst = reinterpret_cast<float*>(o.data) + o.row(bh, start + query) + 4 * VW * g;
+#pragma unroll
+    for (int f = 0; f < 4 * VW; f += 4) {
+        f32x4 x;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) x[j] = oacc[(f + j) % VW][(f + j) / VW];
+        *reinterpret_cast<f32x4*>(dst + f) = x;
     }
 }
 
@@ -320,19 +461,35 @@ static void launch_fixed_mfma(const View& q, const View& k, const View& v, const
                        tokens, nblocks, scale * kLog2e, causal);
 }
 
+template <int D>
+static void launch_fixed_f32_mfma(const View& q, const View& k, const View& v, const OutView& o, int tokens,
+                                  int nblocks, int bh_count, float scale, int causal, hipStream_t stream) {
+    hipLaunchKernelGGL((fixed_block_f32_mfma_kernel<D>), dim3(bh_count * nblocks), dim3(256), 0, stream, q, k, v, o,
+                       tokens, nblocks, scale, causal);
+}
+
 template <typename T>
 int launch_fixed_t(int head_dim, const View& q, const View& k, const View& v, const OutView& o, int tokens,
                    int bh_count, float scale, int causal, const MaskView& mask, hipStream_t stream) {
     const int nblocks = (tokens + 63) / 64;
     const dim3 grid(bh_count * nblocks);
-    if constexpr (!std::is_same<T, float>::value) {
-        // 16-byte row loads and 8-byte output stores need aligned rows
-        auto aligned = [](const char* p, int64_t sb, int64_t sh, int64_t st, int bytes) {
-            const int64_t unit = bytes / (int64_t)sizeof(T);
-            return reinterpret_cast<uintptr_t>(p) % bytes == 0 && sb % unit == 0 && sh % unit == 0 && st % unit == 0;
-        };
-        const bool rows16 = aligned(q.data, q.sb, q.sh, q.st, 16) && aligned(k.data, k.sb, k.sh, k.st, 16) &&
-                            aligned(v.data, v.sb, v.sh, v.st, 16) && aligned(o.data, o.sb, o.sh, o.st, 8);
+    auto aligned = [](const char* p, int64_t sb, int64_t sh, int64_t st, int bytes) {
+        const int64_t unit = bytes / (int64_t)sizeof(T);
+        return reinterpret_cast<uintptr_t>(p) % bytes == 0 && sb % unit == 0 && sh % unit == 0 && st % unit == 0;
+    };
+    // 16-byte row loads and stores need 16-byte aligned rows (the output of
+    // the 16-bit kernel: 2 * head_dim / 32 bytes per store)
+    const int out_bytes = std::is_same<T, float>::value ? 16 : 2 * head_dim / 32;
+    const bool rows16 = aligned(q.data, q.sb, q.sh, q.st, 16) && aligned(k.data, k.sb, k.sh, k.st, 16) &&
+                        aligned(v.data, v.sb, v.sh, v.st, 16) && aligned(o.data, o.sb, o.sh, o.st, out_bytes);
+    if constexpr (std::is_same<T, float>::value) {
+        if (mask.kind == PISA_MASK_NONE && rows16) {
+            if (head_dim == 32) launch_fixed_f32_mfma<32>(q, k, v, o, tokens, nblocks, bh_count, scale, causal, stream);
+            else if (head_dim == 64) launch_fixed_f32_mfma<64>(q, k, v, o, tokens, nblocks, bh_count, scale, causal, stream);
+            else launch_fixed_f32_mfma<128>(q, k, v, o, tokens, nblocks, bh_count, scale, causal, stream);
+            return pisa_host::check_launch("fixed_block_f32_mfma_kernel");
+        }
+    } else {
         if (mask.kind == PISA_MASK_NONE && rows16) {  // the reference's Triton path: no mask (dispatch.py:50-79)
             if (head_dim == 32) launch_fixed_mfma<T, 32>(q, k, v, o, tokens, nblocks, bh_count, scale, causal, stream);
             else if (head_dim == 64) launch_fixed_mfma<T, 64>(q, k, v, o, tokens, nblocks, bh_count, scale, causal, stream);

@@ -417,6 +417,32 @@ def test_fixed_block_matches_oracle(native, dtype, head_dim, tokens, causal):
     assert_close(np32(out), expected, tol, tol, "fixed block")
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_fixed_block_replays_in_a_hip_graph(native, dtype):
+    """The fixed-block entry point launches only its kernel, on the caller's stream, so callers
+    (and bench.py's C1 kernel timing) can capture it in a HIP graph: every replay, with other
+    eager work and synchronisations between replays, equals the eager result bit for bit."""
+    gen = torch.Generator().manual_seed(5)
+    q, k, v = (torch.randn((1, 8, 4096, 64), generator=gen).to(dtype).cuda() for _ in range(3))
+    eager = native.fixed_block_attention(q, k, v, 0.125)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        native.fixed_block_attention(q, k, v, 0.125)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        captured = native.fixed_block_attention(q, k, v, 0.125)
+    for replay in range(4):
+        other = native.fixed_block_attention(k, q, v, 0.25 + replay)  # eager work between replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(captured, eager), f"replay {replay}"
+        assert not torch.equal(other, eager)
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_fixed_block_16bit_paths_on_large_and_unaligned_inputs(native, dtype):
     """Many blocks through the matrix-core kernel (B=2 H=16 T=4096 D=128, a ComfyUI-sized call),
