@@ -27,7 +27,7 @@ from typing import Optional
 import torch
 
 from . import _lib
-from ._lib import LIB, check, dtype_code, grid, ptr, stream_of, view3, view4
+from ._lib import LIB, check, dtype_code, grid, on_device, ptr, stream_of, view3, view4
 
 __version__ = "1.0.0"
 
@@ -138,7 +138,7 @@ def _check_exact_and_sink(exact_blocks, blocks: int, sink_block) -> None:
 def _launch_pisa(q4, k4, v4, out4, token_grid, exact_blocks, scale, sink_block, stats_mode, route_mode,
                  first_order, debug_indices=None, debug_scores=None):
     batch, heads, tokens, head_dim = q4.shape
-    with torch.cuda.device(q4.device):
+    with on_device(q4.device):
         ws_bytes = LIB.pisa_hip_forward_workspace_bytes(batch, heads, tokens, head_dim, exact_blocks)
         workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=q4.device)
         check(
@@ -155,7 +155,7 @@ def _launch_pisa(q4, k4, v4, out4, token_grid, exact_blocks, scale, sink_block, 
 def _launch_dense(q4, k4, v4, out4, scale):
     batch, heads, q_tokens, head_dim = q4.shape
     kv_tokens = k4.shape[2]
-    with torch.cuda.device(q4.device):
+    with on_device(q4.device):
         ws_bytes = LIB.attn_hip_dense_workspace_bytes(batch, heads, kv_tokens, head_dim)
         workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=q4.device)
         check(
@@ -172,10 +172,13 @@ _MASK_KINDS = {torch.bool: _lib.MASK_BOOL, torch.float32: _lib.MASK_ADD_F32, tor
                torch.bfloat16: _lib.MASK_ADD_BF16}
 
 
+_NO_MASK = _lib.PisaMask(None, _lib.MASK_NONE, 1, 0, 0, 0, 0)  # passed by value: one shared instance
+
+
 def _mask_struct(mask: torch.Tensor | None) -> _lib.PisaMask:
     """pisa_mask of a [B', H', T, T] view (0 strides broadcast; B' * H' = the kernel's B*H)."""
     if mask is None:
-        return _lib.PisaMask(None, _lib.MASK_NONE, 1, 0, 0, 0, 0)
+        return _NO_MASK
     if mask.ndim != 4 or mask.dtype not in _MASK_KINDS:
         raise ValueError("the fixed-block mask view must be 4-D bool/float32/float16/bfloat16")
     sb, sh, sq, sk = mask.stride()
@@ -184,7 +187,7 @@ def _mask_struct(mask: torch.Tensor | None) -> _lib.PisaMask:
 
 def _launch_fixed_block(q4, k4, v4, out4, scale, causal, mask=None):
     batch, heads, tokens, head_dim = q4.shape
-    with torch.cuda.device(q4.device):
+    with on_device(q4.device):
         check(
             LIB.attn_hip_fixed_block_forward_masked(
                 dtype_code(q4.dtype), batch, heads, tokens, head_dim, BLOCK_SIZE,
@@ -389,7 +392,7 @@ def _block_stats(q, k, v, mode, out_dtype):
     cov = mode != _lib.STATS_MEANS
     h_sum = q.new_empty((bh, head_dim, head_dim), dtype=torch.float32) if cov else None
     h_norm = q.new_empty((bh, blocks), dtype=torch.float32) if cov else None
-    with torch.cuda.device(q.device):
+    with on_device(q.device):
         ws_bytes = LIB.pisa_hip_block_stats_workspace_bytes(batch, heads, tokens, head_dim) if cov else 0
         workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
         check(
@@ -562,7 +565,7 @@ def route_topk(q_centroids: torch.Tensor, k_centroids: torch.Tensor, h_norm: tor
     hn = None if h_norm is None else h_norm.float().contiguous()
     indices = torch.empty((bh, blocks, max(exact_blocks, 1)), dtype=torch.int32, device=qc.device)
     scores = torch.empty((bh, blocks, blocks), dtype=torch.float32, device=qc.device)
-    with torch.cuda.device(qc.device):
+    with on_device(qc.device):
         check(
             LIB.pisa_hip_route_topk(bh, blocks, head_dim, qc.data_ptr(), kc.data_ptr(), ptr(hn), int(round_bf16),
                                     float(scale), -2 if sink_block is None else int(sink_block), int(exact_blocks),
@@ -638,11 +641,11 @@ class PisaPlan:
                 self.workspace.data_ptr(), self.workspace_bytes, stream_of(self.device))
 
     def prepare(self) -> None:
-        with torch.cuda.device(self.device):
+        with on_device(self.device):
             check(LIB.pisa_hip_prepare(*self._args()), "pisa_hip_prepare")
 
     def attend(self) -> torch.Tensor:
-        with torch.cuda.device(self.device):
+        with on_device(self.device):
             check(LIB.pisa_hip_attend(*self._args()), "pisa_hip_attend")
         return self.tensors[3]
 
@@ -771,7 +774,7 @@ class _NativeNamespace:
         batch, heads, tokens, head_dim = q.shape
         side = _spatial_side(tokens)
         packed = [torch.empty((batch * heads, tokens, head_dim), dtype=q.dtype, device=q.device) for _ in range(3)]
-        with torch.cuda.device(q.device):
+        with on_device(q.device):
             check(
                 LIB.pisa_hip_pack_spatial_qkv(
                     dtype_code(q.dtype), batch, heads, tokens, head_dim, view4(q), view4(k), view4(v),
@@ -793,7 +796,7 @@ class _NativeNamespace:
         _check_native("output", output, (batch * heads, tokens, head_dim), (torch.bfloat16, torch.float16))
         side = _spatial_side(tokens)
         out = output.new_empty((batch, tokens, heads * head_dim))
-        with torch.cuda.device(output.device):
+        with on_device(output.device):
             check(
                 LIB.pisa_hip_unpack_spatial_output(
                     dtype_code(output.dtype), batch, heads, tokens, head_dim, output.data_ptr(),
@@ -820,7 +823,7 @@ class _NativeNamespace:
         _check_native("correction", correction, rows, (torch.float32,), device)
         side = _spatial_side(tokens)
         out = exact_output.new_empty((batch, tokens, heads * head_dim))
-        with torch.cuda.device(device):
+        with on_device(device):
             check(
                 LIB.pisa_hip_fuse_spatial_epilogue(
                     dtype_code(exact_output.dtype), batch, heads, tokens, head_dim,

@@ -9,6 +9,7 @@ library has not been built - there is no fallback implementation.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import pathlib
 
@@ -163,9 +164,10 @@ def check(status: int, what: str) -> None:
 
 def view4(tensor: torch.Tensor) -> PisaView:
     """[B, H, T, D] tensor with unit D stride."""
-    if tensor.stride(3) != 1:
+    sb, sh, st, sd = tensor.stride()
+    if sd != 1:
         raise ValueError("head_dim must have unit stride")
-    return PisaView(tensor.data_ptr(), tensor.stride(0), tensor.stride(1), tensor.stride(2))
+    return PisaView(tensor.data_ptr(), sb, sh, st)
 
 
 def view3(tensor: torch.Tensor) -> PisaView:
@@ -179,8 +181,23 @@ def grid(frames: int = 0, height: int = 0, width: int = 0) -> PisaTokenGrid:
     return PisaTokenGrid(frames, height, width)
 
 
+# torch's raw current-stream query (what its own compiled kernels launch on);
+# the public torch.cuda.current_stream builds a Stream object per call
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_of(device: torch.device) -> int:
+    """hipStream_t (as an int) of the current stream of `device`."""
+    if _raw_stream is not None:
+        return _raw_stream(device.index if device.index is not None else torch.cuda.current_device())
     return torch.cuda.current_stream(device).cuda_stream
+
+
+def on_device(device: torch.device):
+    """Device guard around a launch; a no-op when `device` is already the current device."""
+    if device.index is None or device.index == torch.cuda.current_device():
+        return contextlib.nullcontext()
+    return torch.cuda.device(device)
 
 
 def ptr(tensor: torch.Tensor | None) -> int | None:
