@@ -138,8 +138,6 @@ struct NextBlock {
     int bh, qb, sub, nt;
 };
 typedef __attribute__((address_space(3))) char lds_char;
-constexpr int kWaitLgkm0 = 0xC07F;  // s_waitcnt lgkmcnt(0) (vmcnt, expcnt at their maximum)
-constexpr int kWaitVm0 = 0x0F70;    // s_waitcnt vmcnt(0) (lgkmcnt, expcnt at their maximum)
 
 // Direct-to-LDS copy of 16 bytes per lane: lane l's 16 bytes at gptr land at
 // LDS byte address lds_base + 16 l.  Written as inline asm so that the

@@ -29,6 +29,12 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kBlock = PISA_BLOCK_SIZE;  // tokens per PISA block
+// s_waitcnt immediates (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4,
+// lgkmcnt 11:8) for the explicit waits around the direct-to-LDS copies, which
+// the compiler's counters do not model.  tests/test_build_guards.py checks
+// that the assembler prints them as the single waits named here.
+constexpr int kWaitLgkm0 = 0xC07F;  // s_waitcnt lgkmcnt(0) (vmcnt, expcnt at their maximum)
+constexpr int kWaitVm0 = 0x0F70;    // s_waitcnt vmcnt(0) (lgkmcnt, expcnt at their maximum)
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 
