@@ -132,15 +132,32 @@ struct StatsPlan {
     int blocks, npad, chunks, chunk_blocks, mask_words;
 };
 
+// The statistics grid is bh x chunks workgroups of chunk_blocks consecutive
+// blocks; two workgroups fit a CU (LDS), so 512 run at once.  The chunking
+// minimises (rounds of 512 workgroups) x (blocks of a workgroup + its start-up,
+// about three blocks' time): a grid of 520 workgroups would run its last 8 as
+// a second round of a whole workgroup's time (C5: 40 heads x 13 chunks of 40
+// blocks; 12 chunks of 43 fit one round).
 static StatsPlan plan_stats(int bh, int tokens) {
+    constexpr int kSlots = 512;
+    constexpr int kStartBlocks = 3;
     StatsPlan p;
     p.blocks = (tokens + pisa::kBlock - 1) / pisa::kBlock;
     p.npad = (p.blocks + 63) / 64 * 64;
-    int target = (512 + bh - 1) / bh;
-    if (target < 1) target = 1;
-    if (target > p.blocks) target = p.blocks;
-    p.chunk_blocks = (p.blocks + target - 1) / target;
-    p.chunks = (p.blocks + p.chunk_blocks - 1) / p.chunk_blocks;
+    p.chunk_blocks = p.blocks;
+    p.chunks = 1;
+    int64_t best = -1;
+    for (int c = 1; c <= p.blocks && c <= 1024; ++c) {
+        const int cb = (p.blocks + c - 1) / c;
+        const int cc = (p.blocks + cb - 1) / cb;
+        const int64_t rounds = ((int64_t)bh * cc + kSlots - 1) / kSlots;
+        const int64_t cost = rounds * (cb + kStartBlocks);
+        if (best < 0 || cost < best) {
+            best = cost;
+            p.chunk_blocks = cb;
+            p.chunks = cc;
+        }
+    }
     p.mask_words = (p.blocks + 31) / 32;
     return p;
 }
