@@ -415,11 +415,14 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
     // common half (exact, full block) takes no branch before its maxima, so
     // they are computed in the region of the preceding PV MFMAs; tail chunks
     // and a short last block are transformed and re-maxed on a side path.
-    auto check_half = [&](int x, int row, int mt, f32x16 (&s)[NT], bool enable) -> float {
+    // `plain` (a constant in each inlined copy): chunk x is known to be an
+    // exact full block, so there is no side path at all (with one, the scores
+    // are copied to the registers the two paths merge into, every half).
+    auto check_half = [&](int x, int row, int mt, f32x16 (&s)[NT], bool enable, bool plain) -> float {
         float mx[NT];
         half_max<NT>(s, c, mx);
         float f = c;
-        if (special(x, row)) {
+        if (!plain && special(x, row)) {
             f = transform_half(x, row, mt, s);
             half_max<NT>(s, f, mx);
         }
@@ -466,18 +469,23 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
         load_k_half(kf[0], kptr(1, row1), 0);
         load_v_half(v0, 1);
         prefetch_next();
-        ca = check_half(0, row0, 0, sa, true);
+        ca = check_half(0, row0, 0, sa, true, false);
         // One chunk step: half 0 of chunk cc (scores in sa) beside the scores of
         // half 1, then half 1 beside the scores of the next chunk's half 0.  The
         // last step (`last`, a constant in each inlined copy) has no next chunk:
         // those scores are dead code, and its loads bring the packed H_sum^T
         // fragments of the correction instead.
-        auto chunk_step = [&](int cc, bool last, bool half0_only) __attribute__((always_inline)) {
-            const int row2 = table_row(cc + 2);
-            const bool tail = is_tail(cc);
-            const Src kn = (first_order && last) ? Src{ht_rs, 0} : kptr(cc + 1, row1);
-            const Src vn = (first_order && last) ? Src{ht_rs, 16 * 1024} : vptr(cc + 1, row1);
-            const Src kn2 = (first_order && last) ? Src{ht_rs, 0} : kptr(cc + 2, row2);
+        // `plain`: chunks cc, cc + 1 and cc + 2 are exact blocks and cc, cc + 1
+        // full ones (no tail or short-block tests, direct table rows).
+        auto chunk_step = [&](int cc, bool last, bool half0_only, bool plain) __attribute__((always_inline)) {
+            const int row2 = plain ? (SPARSE ? my_idx[cc + 2] : cc + 2) : table_row(cc + 2);
+            const bool tail = !plain && is_tail(cc);
+            const Src kn = (first_order && last) ? Src{ht_rs, 0}
+                           : plain ? Src{kp_rs, row1 * (int)kBlockBytes} : kptr(cc + 1, row1);
+            const Src vn = (first_order && last) ? Src{ht_rs, 16 * 1024}
+                           : plain ? Src{vp_rs, row1 * (int)kBlockBytes} : vptr(cc + 1, row1);
+            const Src kn2 = (first_order && last) ? Src{ht_rs, 0}
+                            : plain ? Src{kp_rs, row2 * (int)kBlockBytes} : kptr(cc + 2, row2);
             vec8 pf[NT][2];
 
             // ---- first half: scores in sa (issued, masked and max-checked one half earlier)
@@ -486,7 +494,7 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
             load_k_half(kf[1], kn, 1);
             pv_half(0, pf);
             load_v_half(vn, 0);
-            const float cb = half0_only ? c : check_half(cc, row0, 1, sb, true);
+            const float cb = half0_only ? c : check_half(cc, row0, 1, sb, true, plain);
 
             // ---- second half: scores in sb; also scores the next chunk's first half
             if (!last) scores_half(kf[0], sa);
@@ -494,18 +502,23 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
             load_k_half(kf[0], kn2, 0);
             if (!half0_only) pv_half(1, pf);
             load_v_half(vn, 1);
-            if (!last) ca = check_half(cc + 1, row1, 0, sa, true);
+            if (!last) ca = check_half(cc + 1, row1, 0, sa, true, plain);
             row0 = row1;
             row1 = row2;
         };
-        for (int cc = 0; cc + 1 < n_chunks; ++cc) chunk_step(cc, false, false);
+        // Exact chunks before the last two are full blocks (the selection is
+        // ascending, so a short last key block can only be the last exact
+        // chunk) and are followed by exact chunks: they take the plain step.
+        int cc = 0;
+        for (; cc + 3 <= n_exact; ++cc) chunk_step(cc, false, false, true);
+        for (; cc + 1 < n_chunks; ++cc) chunk_step(cc, false, false, false);
         // The last chunk.  A centroid chunk whose second half holds only
         // padding (centroids past the last block: C4's 144 centroids end 16 keys
         // into their third chunk) skips that half's scores, softmax and PV
         // (they would add exactly zero to l, l_tail and O); its loads still go
         // out, unconditionally, so no register keeps two values across a branch.
         const int cl = n_chunks - 1;
-        chunk_step(cl, true, TAIL && is_tail(cl) && table_row(cl) * kBlock + 32 >= a.centroids);
+        chunk_step(cl, true, TAIL && is_tail(cl) && table_row(cl) * kBlock + 32 >= a.centroids, false);
     }
 
     if (n_chunks == 0) prefetch_next();
