@@ -11,6 +11,9 @@ tail, first-order correction, merge, raster output).
 
 Also measured in the same process, in this order:
   * the first call, reported separately (nothing is compiled at run time);
+  * 200 untimed calls: after an idle period the attention kernel runs up to
+    ~20 % slower for ~25 calls, so every region below starts at settled clocks;
+  * the metric: K whole calls after W warm-up calls;
   * the statistics + routing launches (PisaPlan.prepare) and the fused
     attention kernel alone (PisaPlan.attend, one launch), timed with HIP events
     on the stream they run on -> roofline against dense bf16 MFMA peak;
@@ -20,11 +23,8 @@ Also measured in the same process, in this order:
     of one exact 64-key tile step for the whole grid -> exact_tiles_marginal;
   * the dense exact attention kernel of this library on the same shape (the
     1.8x comparator of the north star) and torch's SDPA on the same views;
-  * the metric: K whole calls after W warm-up calls.  It runs after the
-    measurements above, so the GPU is past the clock dip that follows an idle
-    period (after an idle second the attention kernel runs up to ~20 % slower
-    for the next ~25 calls, then settles); the same region timed right after
-    one idle second is reported as call_ms_after_1s_idle;
+  * the metric's region again right after one idle second
+    (call_ms_after_1s_idle);
   * the CPU baseline: the fp32 torch port of the HYD forward
     (oracle.torch_cpu) over the whole call on the host's CPU threads.
 
@@ -508,9 +508,15 @@ def main() -> int:
     # untimed settle: 200 back-to-back calls (~80 ms of GPU work) carry the GPU
     # through the clock dip that follows the idle first call, so every region
     # below is timed at settled clocks
+    call = lambda: mi355x_pisa.forward_spatial_bhtd(q, k, v, exact_blocks=EXACT)  # noqa: E731
     for _ in range(200):
-        mi355x_pisa.forward_spatial_bhtd(q, k, v, exact_blocks=EXACT)
+        call()
     torch.cuda.synchronize()
+
+    # whole call: the metric, K calls after W warm-up calls, timed right after
+    # the settle and before the comparators below (after the seconds of dense
+    # and SDPA work the same calls have run up to 15 % slower)
+    call_ms = time_gpu(call, args.steps, args.warmup)
 
     # stages on the same inputs: prepare (statistics, H_sum reduction, routing) and attend (one kernel)
     out4 = torch.empty((BATCH, TOKENS, HEADS * HEAD_DIM), dtype=q.dtype, device=device)
@@ -534,12 +540,9 @@ def main() -> int:
     sdpa_ms = time_gpu(lambda: torch.nn.functional.scaled_dot_product_attention(q, k, v, scale=scale),
                        max(2, args.steps // 4), 2)
 
-    # whole call: the metric.  It is timed after the stage measurements above, so
-    # the GPU is past the clock dip that follows an idle period (after 1 s idle
-    # the attention kernel runs ~15 % slower for the next ~25 calls); the same
-    # region right after an idle second is reported beside it.
-    call = lambda: mi355x_pisa.forward_spatial_bhtd(q, k, v, exact_blocks=EXACT)  # noqa: E731
-    call_ms = time_gpu(call, args.steps, args.warmup)
+    # the plan's stages reproduce the call bit for bit; then the metric's region
+    # again right after an idle second (after 1 s idle the attention kernel runs
+    # up to ~20 % slower for the next ~25 calls), reported beside it
     torch.testing.assert_close(out4.permute(0, 2, 1, 3).reshape(BATCH, TOKENS, -1), call(), atol=0, rtol=0)
     torch.cuda.synchronize()
     time.sleep(1.0)
