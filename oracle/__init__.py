@@ -16,7 +16,10 @@ tests live in tests/test_oracle.py and tests/test_oracle_pins.py):
   reshape/permute restatement of generic_pisa.py:17-52 and exact round trips.
 * attention.dense_attention -- torch.nn.functional.scaled_dot_product_attention.
 * attention.fixed_block_attention -- a dense softmax with a block-diagonal
-  (and causal) mask (reference.py:227-241 semantics) on tiny inputs.
+  (and causal) mask (reference.py:227-241 semantics) on tiny inputs; the
+  16-bit probability rounding (prob_dtype, triton_kernel.py:92-96) by a block
+  whose probabilities are exactly [1/3, 2/3]: the output is bf16(1/3) resp.
+  fp16(1/3), which rounding before normalising or not rounding cannot give.
 * pisa.block_stats -- textbook means / covariance (float64), ||H_b||_F via
   numpy.linalg.norm, per-block-constant keys give H = 0, bf16 extrema stay
   finite (test_forward.py:172-201).

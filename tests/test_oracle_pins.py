@@ -14,7 +14,10 @@ chosen so that the plausible misreadings of the reference fail:
 * the Triton statistics' dtype rounding of the centred keys
   (pisa_kernel.py:80-81) against fp32 centring (pisa_kernels.cu:222-226);
 * the pre-scaled running mean of block_stats_kernel (pisa_kernels.cu:148-158)
-  against sum-then-scale and against separately rounded products.
+  against sum-then-scale and against separately rounded products;
+* the fixed-block Triton path's rounding of the normalised probabilities to
+  the input dtype (triton_kernel.py:92-96) against rounding before normalising
+  and against no rounding.
 """
 from __future__ import annotations
 
@@ -254,3 +257,24 @@ def test_h3_pack_copies_bit_exactly(tokens, profile):
     ref = torch.stack((tq, tk, tv)) if profile == "qkv" else torch.stack((tk, tv))
     np.testing.assert_array_equal(pk, ref[-2].numpy())
     np.testing.assert_array_equal(pv, ref[-1].numpy())
+
+
+def test_fixed_block_16bit_probabilities_round_after_normalising():
+    """Scores [0, ln 2] in one block give the probabilities [1/3, 2/3]; the Triton kernel rounds
+    the normalised probabilities to the input dtype before P @ V (triton_kernel.py:92-96).  With
+    V = [1, 0] the first output is exactly bf16(1/3) = 0.333984375 (fp16(1/3) = 0.333251953125);
+    rounding the unnormalised exponentials [1, 2] instead, or not rounding, gives 1/3."""
+    from oracle import attention as oatt
+
+    q = np.array([[1.0], [0.0]], dtype=np.float32)
+    k = np.array([[0.0], [np.log(2.0)]], dtype=np.float32)
+    v = np.array([[1.0], [0.0]], dtype=np.float32)
+    bf = oatt.fixed_block_attention(q, k, v, scale=1.0, prob_dtype="bf16")
+    hf = oatt.fixed_block_attention(q, k, v, scale=1.0, prob_dtype="f16")
+    unrounded = oatt.fixed_block_attention(q, k, v, scale=1.0)
+    k_f32_ln2 = float(np.float32(np.log(2.0)))  # the fp32 ln 2 the oracle multiplies
+    third = 1.0 / (1.0 + np.exp(k_f32_ln2))     # softmax weight of key 0
+    assert abs(third - 1.0 / 3.0) < 1e-7
+    assert float(bf[0, 0]) == 0.333984375
+    assert float(hf[0, 0]) == 0.333251953125
+    assert abs(float(unrounded[0, 0]) - third) < 1e-7
