@@ -705,6 +705,8 @@ __global__ __launch_bounds__(256) void kv_pack_kernel(View k, View v, TokenMap m
     const bool live_d = pc * 8 < d_real;      // d_real is a multiple of 8
     T* kdst = reinterpret_cast<T*>(kp) + ((int64_t)bh * kv_blocks + j) * D * kBlock;
     T* vdst = reinterpret_cast<T*>(vp) + ((int64_t)bh * kv_blocks + j) * D * kBlock;
+    const int base = map.block_base(j);          // raster token of row r: base + intra_offset(r)
+    const int last = kv_tokens - 1 - j * kBlock;  // rows past the end read the last token
     for (int r = r0 * 4; r < kBlock; r += kRowsPerPass * 4) {
         // the 8 loads of the 4 rows go out together and unconditionally (rows
         // past kv_tokens re-read the last token, dims past d_real the first
@@ -715,7 +717,7 @@ __global__ __launch_bounds__(256) void kv_pack_kernel(View k, View v, TokenMap m
         for (int rr = 0; rr < 4; ++rr) {
             const int key = j * kBlock + r + rr;
             live[rr] = key < kv_tokens && live_d;
-            const int tok = map(min(key, kv_tokens - 1));
+            const int tok = base + map.intra_offset(min(r + rr, last));
             const int dc = live_d ? pc * 8 : 0;
             kx[rr] = load8<vec8>(k.data + (k.row(bh, tok) + dc) * sizeof(T));
             x[rr] = load8<vec8>(v.data + (v.row(bh, tok) + dc) * sizeof(T));

@@ -80,10 +80,13 @@ __global__ __launch_bounds__(kStatsThreads) __attribute__((amdgpu_waves_per_eu(2
         const int start = b * kBlock;
         const int len = min(kBlock, a.tokens - start);
         const int64_t off = (c16 * 8) * (int64_t)sizeof(T);
+        // raster token of row r = block_base(b) + intra_offset(r): the map's
+        // divisions run once per block (wave-uniform), not once per row
+        const int base = a.map.block_base(b);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int tok = rq * 4 + r;
-            const int raster = a.map(start + min(tok, len - 1));
+            const int raster = base + a.map.intra_offset(min(tok, len - 1));
             qv[r] = load8<vec8>(a.q.data + a.q.row(bh, raster) * sizeof(T) + off);
             kv[r] = load8<vec8>(a.k.data + a.k.row(bh, raster) * sizeof(T) + off);
             vv[r] = load8<vec8>(a.v.data + a.v.row(bh, raster) * sizeof(T) + off);
@@ -340,6 +343,7 @@ __global__ __launch_bounds__(256) void stats_means_kernel(StatsArgs a) {
     const int pc = t % P;
     const int rr = t / P;
     const bool mapped = t < R * P;
+    const int base = a.map.block_base(b);  // raster token of row r: base + intra_offset(r)
     float sq[8], sk[8], sv[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) sq[e] = sk[e] = sv[e] = 0.0f;
@@ -349,7 +353,7 @@ __global__ __launch_bounds__(256) void stats_means_kernel(StatsArgs a) {
         for (int pass = 0; pass < kPasses; ++pass) {
             const int r = pass * R + rr;
             if (r < len) {
-                const int raster = a.map(start + r);
+                const int raster = base + a.map.intra_offset(r);
                 const vec8 x = load8<vec8>(a.q.data + a.q.row(bh, raster) * sizeof(T) + off);
                 const vec8 y = load8<vec8>(a.k.data + a.k.row(bh, raster) * sizeof(T) + off);
                 const vec8 z = load8<vec8>(a.v.data + a.v.row(bh, raster) * sizeof(T) + off);
