@@ -92,11 +92,6 @@ __device__ __forceinline__ float add_xor32(float x) { const float2 p = pair_xor3
 __device__ __forceinline__ float add_xor16(float x) { const float2 p = pair_xor16(x); return p.x + p.y; }
 __device__ __forceinline__ float max_xor32(float x) { const float2 p = pair_xor32(x); return fmaxf(p.x, p.y); }
 
-__device__ __forceinline__ float wave_max(float x) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
-    return x;
-}
 __device__ __forceinline__ float wave_sum(float x) {
     x = add_xor32(x);
     x = add_xor16(x);
