@@ -468,7 +468,6 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
         scores_half(kf[0], sa);
         load_k_half(kf[0], kptr(1, row1), 0);
         load_v_half(v0, 1);
-        prefetch_next();
         ca = check_half(0, row0, 0, sa, true, false);
         // One chunk step: half 0 of chunk cc (scores in sa) beside the scores of
         // half 1, then half 1 beside the scores of the next chunk's half 0.  The
@@ -521,7 +520,16 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
         chunk_step(cl, true, TAIL && is_tail(cl) && table_row(cl) * kBlock + 32 >= a.centroids, false);
     }
 
-    if (n_chunks == 0) prefetch_next();
+    // The copies of the next block's query rows and first chunk go out here,
+    // after an explicit wait for this block's last loads (the correction's
+    // fragments, needed next anyway): the copies are hidden from the compiler's
+    // counters, so every wait issued after them also waits for them.  Issued in
+    // the prologue, they held the block's first chunk waits; here they land
+    // during the correction and the stores, which wait for nothing.
+    if constexpr (PERSIST) {
+        __builtin_amdgcn_s_waitcnt(kWaitVm0);
+        prefetch_next();
+    }
 
     // ---- epilogue: normalise, add the first-order correction one 32-dim
     // tile at a time (keeps only 32 extra accumulators live), store the real
