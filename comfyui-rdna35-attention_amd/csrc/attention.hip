@@ -134,6 +134,9 @@ __device__ __forceinline__ void probs_half(const f32x16 (&s)[NT], float c, const
 // The block a persistent wave runs next (nt = 0: none): its query rows and the
 // key and value fragments of its first chunk are copied to the wave's LDS
 // while the current block runs.
+// Chunk-step kinds of the attention loop (see check_half / chunk_step).
+constexpr int kStepGeneral = 0, kStepExact = 1, kStepTail = 2;
+
 struct NextBlock {
     int bh, qb, sub, nt;
 };
@@ -367,21 +370,9 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
     // Whether half chunks of chunk x (table row `row`) need transform_half: tail
     // chunks and a short last key block (wave-uniform).
     auto special = [&](int x, int row) { return is_tail(x) || (row + 1) * kBlock > a.kv_tokens; };
-    // Masks / tail bias of half mt of chunk x (row = its table row); returns
-    // the factor that converts the resulting scores to log2 units.
-    auto transform_half = [&](int x, int row, int mt, f32x16 (&s)[NT]) -> float {
-        if (!is_tail(x)) {
-            if ((row + 1) * kBlock > a.kv_tokens) {  // wave-uniform: only a short last block
-#pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    const int key = row * kBlock + mt * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
-                    if (key >= a.kv_tokens)
-#pragma unroll
-                        for (int nt = 0; nt < NT; ++nt) s[nt][v] = -__builtin_inff();
-                }
-            }
-            return c;
-        }
+    // Tail bias of half mt of the centroid chunk in table row `row`; the
+    // scores come out in log2 units (returns the factor 1).
+    auto transform_tail = [&](int row, int mt, f32x16 (&s)[NT]) -> float {
         // centroid jc = base + bit (base = 64row + 32mt): selected blocks and
         // padding -> -inf, others + log2(len_jc) (scores moved to log2 units
         // here).  One bias per accumulator row, shared by the query tiles: the
@@ -410,21 +401,45 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
             for (int nt = 0; nt < NT; ++nt) s[nt][v] = fmaf(s[nt][v], c, bias[v]);
         return 1.0f;
     };
+    // Masks / tail bias of half mt of chunk x (row = its table row); returns
+    // the factor that converts the resulting scores to log2 units.
+    auto transform_half = [&](int x, int row, int mt, f32x16 (&s)[NT]) -> float {
+        if (!is_tail(x)) {
+            if ((row + 1) * kBlock > a.kv_tokens) {  // wave-uniform: only a short last block
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const int key = row * kBlock + mt * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
+                    if (key >= a.kv_tokens)
+#pragma unroll
+                        for (int nt = 0; nt < NT; ++nt) s[nt][v] = -__builtin_inff();
+                }
+            }
+            return c;
+        }
+        return transform_tail(row, mt, s);
+    };
 
     // Column maxima of half mt of chunk x, then the running-max update.  The
     // common half (exact, full block) takes no branch before its maxima, so
     // they are computed in the region of the preceding PV MFMAs; tail chunks
     // and a short last block are transformed and re-maxed on a side path.
-    // `plain` (a constant in each inlined copy): chunk x is known to be an
-    // exact full block, so there is no side path at all (with one, the scores
-    // are copied to the registers the two paths merge into, every half).
-    auto check_half = [&](int x, int row, int mt, f32x16 (&s)[NT], bool enable, bool plain) -> float {
+    // `kind` (a constant in each inlined copy): kStepExact, chunk x is known to
+    // be an exact full block, so there is no side path at all (with one, the
+    // scores are copied to the registers the two paths merge into, every
+    // half); kStepTail, x is known to be a centroid chunk, transformed
+    // unconditionally and maxed once; kStepGeneral tests.
+    auto check_half = [&](int x, int row, int mt, f32x16 (&s)[NT], bool enable, int kind) -> float {
         float mx[NT];
-        half_max<NT>(s, c, mx);
         float f = c;
-        if (!plain && special(x, row)) {
-            f = transform_half(x, row, mt, s);
+        if (kind == kStepTail) {
+            f = transform_tail(row, mt, s);
             half_max<NT>(s, f, mx);
+        } else {
+            half_max<NT>(s, c, mx);
+            if (kind == kStepGeneral && special(x, row)) {
+                f = transform_half(x, row, mt, s);
+                half_max<NT>(s, f, mx);
+            }
         }
         rescale_to<NT, MD>(mx, enable, m, l, lt, o);
         return f;
@@ -468,23 +483,29 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
         scores_half(kf[0], sa);
         load_k_half(kf[0], kptr(1, row1), 0);
         load_v_half(v0, 1);
-        ca = check_half(0, row0, 0, sa, true, false);
+        ca = check_half(0, row0, 0, sa, true, kStepGeneral);
         // One chunk step: half 0 of chunk cc (scores in sa) beside the scores of
         // half 1, then half 1 beside the scores of the next chunk's half 0.  The
         // last step (`last`, a constant in each inlined copy) has no next chunk:
         // those scores are dead code, and its loads bring the packed H_sum^T
         // fragments of the correction instead.
-        // `plain`: chunks cc, cc + 1 and cc + 2 are exact blocks and cc, cc + 1
-        // full ones (no tail or short-block tests, direct table rows).
-        auto chunk_step = [&](int cc, bool last, bool half0_only, bool plain) __attribute__((always_inline)) {
-            const int row2 = plain ? (SPARSE ? my_idx[cc + 2] : cc + 2) : table_row(cc + 2);
-            const bool tail = !plain && is_tail(cc);
+        // `kind`: kStepExact, chunks cc, cc + 1 and cc + 2 are exact blocks and
+        // cc, cc + 1 full ones (no tail or short-block tests, direct table
+        // rows); kStepTail, chunks cc and cc + 1 are centroid chunks (as is
+        // cc + 2, or the last one re-read).
+        auto chunk_step = [&](int cc, bool last, bool half0_only, int kind) __attribute__((always_inline)) {
+            const bool exact_k = kind == kStepExact, tail_k = kind == kStepTail;
+            const int row2 = exact_k ? (SPARSE ? my_idx[cc + 2] : cc + 2) : table_row(cc + 2);
+            const bool tail = tail_k || (!exact_k && is_tail(cc));
             const Src kn = (first_order && last) ? Src{ht_rs, 0}
-                           : plain ? Src{kp_rs, row1 * (int)kBlockBytes} : kptr(cc + 1, row1);
+                           : exact_k ? Src{kp_rs, row1 * (int)kBlockBytes}
+                           : tail_k  ? Src{kc_rs, row1 * (int)kBlockBytes} : kptr(cc + 1, row1);
             const Src vn = (first_order && last) ? Src{ht_rs, 16 * 1024}
-                           : plain ? Src{vp_rs, row1 * (int)kBlockBytes} : vptr(cc + 1, row1);
+                           : exact_k ? Src{vp_rs, row1 * (int)kBlockBytes}
+                           : tail_k  ? Src{vc_rs, row1 * (int)kBlockBytes} : vptr(cc + 1, row1);
             const Src kn2 = (first_order && last) ? Src{ht_rs, 0}
-                            : plain ? Src{kp_rs, row2 * (int)kBlockBytes} : kptr(cc + 2, row2);
+                            : exact_k ? Src{kp_rs, row2 * (int)kBlockBytes}
+                            : tail_k  ? Src{kc_rs, row2 * (int)kBlockBytes} : kptr(cc + 2, row2);
             vec8 pf[NT][2];
 
             // ---- first half: scores in sa (issued, masked and max-checked one half earlier)
@@ -493,7 +514,7 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
             load_k_half(kf[1], kn, 1);
             pv_half(0, pf);
             load_v_half(vn, 0);
-            const float cb = half0_only ? c : check_half(cc, row0, 1, sb, true, plain);
+            const float cb = half0_only ? c : check_half(cc, row0, 1, sb, true, kind);
 
             // ---- second half: scores in sb; also scores the next chunk's first half
             if (!last) scores_half(kf[0], sa);
@@ -501,23 +522,27 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
             load_k_half(kf[0], kn2, 0);
             if (!half0_only) pv_half(1, pf);
             load_v_half(vn, 1);
-            if (!last) ca = check_half(cc + 1, row1, 0, sa, true, plain);
+            if (!last) ca = check_half(cc + 1, row1, 0, sa, true, kind);
             row0 = row1;
             row1 = row2;
         };
         // Exact chunks before the last two are full blocks (the selection is
         // ascending, so a short last key block can only be the last exact
-        // chunk) and are followed by exact chunks: they take the plain step.
+        // chunk) and are followed by exact chunks: they take the plain exact
+        // step.  The last two exact chunks take the general step, and centroid
+        // chunks followed by centroid chunks the centroid step.
         int cc = 0;
-        for (; cc + 3 <= n_exact; ++cc) chunk_step(cc, false, false, true);
-        for (; cc + 1 < n_chunks; ++cc) chunk_step(cc, false, false, false);
+        for (; cc + 3 <= n_exact; ++cc) chunk_step(cc, false, false, kStepExact);
+        for (; cc + 1 < n_chunks && (!TAIL || cc < n_exact); ++cc) chunk_step(cc, false, false, kStepGeneral);
+        if constexpr (TAIL)
+            for (; cc + 1 < n_chunks; ++cc) chunk_step(cc, false, false, kStepTail);
         // The last chunk.  A centroid chunk whose second half holds only
         // padding (centroids past the last block: C4's 144 centroids end 16 keys
         // into their third chunk) skips that half's scores, softmax and PV
         // (they would add exactly zero to l, l_tail and O); its loads still go
         // out, unconditionally, so no register keeps two values across a branch.
         const int cl = n_chunks - 1;
-        chunk_step(cl, true, TAIL && is_tail(cl) && table_row(cl) * kBlock + 32 >= a.centroids, false);
+        chunk_step(cl, true, TAIL && is_tail(cl) && table_row(cl) * kBlock + 32 >= a.centroids, kStepGeneral);
     }
 
     // The copies of the next block's query rows and first chunk go out here,
