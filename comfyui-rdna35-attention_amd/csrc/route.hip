@@ -19,9 +19,10 @@
 // selected, and keys equal to T are taken in ascending block order until k
 // are chosen - i.e. the k largest scores with ties to the lowest index,
 // independent of scheduling, so the selection is reproducible bit for bit.
-// Four rows are searched interleaved, each stopping at the first prefix with
-// exactly k keys at or above it.  Indices are written in ascending
-// order, with the selection bit mask the attention tail uses.
+// Four rows are searched together, with no branch between them, until every
+// row's prefix has exactly k keys at or above it.  Indices are written in
+// ascending order, with the selection bit mask the attention tail uses (lane w
+// writing word w).  h_norm is loaded before the scores are formed.
 //
 // Semantics: native/rdna35_pisa_ck/rdna35_pisa_ck/__init__.py:258-269 (HYD:
 // bf16 centroids, fp32 products, + ln(h_norm + 1e-5), sink = +inf, topk then
@@ -85,6 +86,13 @@ __global__ __launch_bounds__(64 * kRouteWaves) void route_topk_kernel(RouteArgs 
     const int i0 = (blockIdx.x - bh * row_tiles) * kRouteTile;
     const int stride = N + 1;
     const bool rnd = a.round_bf16 != 0;
+    // h_norm of the candidates l, l+64, ... (HYD bias), loaded before the
+    // scores so its latency hides behind them; indices clamped into the row
+    // (candidates past N get key 0 whatever their bias)
+    const bool has_h = a.hnorm != nullptr;
+    float hn[PL];
+#pragma unroll
+    for (int u = 0; u < PL; ++u) hn[u] = has_h ? a.hnorm[(int64_t)bh * N + min(lane + 64 * u, N - 1)] : 0.0f;
 
     // ---- scores of rows i0 .. i0+15 against every candidate tile.  K step s
     // of lane group g multiplies dim 16(s/4) + 4g + s%4 when D is a multiple
@@ -207,16 +215,13 @@ __global__ __launch_bounds__(64 * kRouteWaves) void route_topk_kernel(RouteArgs 
         }
     }
     }
+    float bias[PL];
+#pragma unroll
+    for (int u = 0; u < PL; ++u) bias[u] = has_h ? logf(hn[u] + 1e-5f) : 0.0f;
     __syncthreads();
 
     // ---- scale, HYD bias, sink; selection of rows 4 wave .. 4 wave + 3
     const int sink_j = a.sink == PISA_NO_SINK ? -1 : (a.sink < 0 ? N + a.sink : a.sink);
-    float bias[PL];
-#pragma unroll
-    for (int u = 0; u < PL; ++u) {
-        const int j = lane + 64 * u;
-        bias[u] = (a.hnorm && j < N) ? logf(a.hnorm[(int64_t)bh * N + j] + 1e-5f) : 0.0f;
-    }
     const uint64_t lt_mask = (1ull << lane) - 1ull;
     const int k = a.k;
     {
@@ -244,11 +249,13 @@ __global__ __launch_bounds__(64 * kRouteWaves) void route_topk_kernel(RouteArgs 
             }
             return;
         }
-        // k-th largest key of each row: largest T with #{key >= T} >= k; the
-        // rows' bit-by-bit searches are independent and run interleaved.  A row
-        // whose prefix already has exactly k keys at or above it is finished:
-        // those k keys are the k largest, so the selection is the same as with
-        // the full 32-bit threshold.
+        // k-th largest key of each row: largest T with #{key >= T} >= k, found
+        // bit by bit for the four rows together, without branches between them.
+        // Once a row's prefix has exactly k keys at or above it, those k keys
+        // are its k largest and every later step keeps #{key >= T} == k (a
+        // candidate is taken only when its count is >= k, and it is <= k), so
+        // the rows still searched after that select the same set; the search
+        // ends when every row has reached that point (or after bit 0).
         uint32_t T_k[kRouteRows];
         bool done[kRouteRows];
 #pragma unroll
@@ -260,13 +267,12 @@ __global__ __launch_bounds__(64 * kRouteWaves) void route_topk_kernel(RouteArgs 
             bool all_done = true;
 #pragma unroll
             for (int rr = 0; rr < kRouteRows; ++rr) {
-                if (done[rr]) continue;  // wave-uniform
                 const uint32_t cand = T_k[rr] | (1u << b);
                 int cnt = 0;
 #pragma unroll
                 for (int u = 0; u < PL; ++u) cnt += __popcll(__ballot(key[rr][u] >= cand));
-                if (cnt >= k) T_k[rr] = cand;
-                done[rr] = cnt == k;
+                T_k[rr] = cnt >= k ? cand : T_k[rr];
+                done[rr] = done[rr] || cnt == k;
                 all_done = all_done && done[rr];
             }
             if (all_done) break;
@@ -280,22 +286,21 @@ __global__ __launch_bounds__(64 * kRouteWaves) void route_topk_kernel(RouteArgs 
             for (int u = 0; u < PL; ++u) gt += __popcll(__ballot(key[rr][u] > T_k[rr]));
             int ties_left = k - gt;  // keys equal to T_k still to take, lowest index first
             int32_t* out_idx = a.idx + ((int64_t)bh * N + i) * k;
-            uint32_t* mask = a.selmask ? a.selmask + ((int64_t)bh * N + i) * a.mask_words : nullptr;
             int before = 0;
+            uint32_t word = 0u;  // mask word `lane` of the row
 #pragma unroll
             for (int u = 0; u < PL; ++u) {
                 const uint64_t tie = __ballot(key[rr][u] == T_k[rr]);
                 const int tie_rank = __popcll(tie & lt_mask);
                 const bool sel = key[rr][u] > T_k[rr] || (key[rr][u] == T_k[rr] && tie_rank < ties_left);
-                ties_left -= min(ties_left, __popcll(tie));
+                ties_left -= min(ties_left, static_cast<int>(__popcll(tie)));
                 const uint64_t bal = __ballot(sel);
                 if (sel) out_idx[before + __popcll(bal & lt_mask)] = lane + 64 * u;
-                if (mask && lane == 0) {
-                    if (2 * u < a.mask_words) mask[2 * u] = static_cast<uint32_t>(bal);
-                    if (2 * u + 1 < a.mask_words) mask[2 * u + 1] = static_cast<uint32_t>(bal >> 32);
-                }
+                word = lane == 2 * u ? static_cast<uint32_t>(bal) : word;
+                word = lane == 2 * u + 1 ? static_cast<uint32_t>(bal >> 32) : word;
                 before += __popcll(bal);
             }
+            if (a.selmask && lane < a.mask_words) a.selmask[((int64_t)bh * N + i) * a.mask_words + lane] = word;
         }
     }
 }
