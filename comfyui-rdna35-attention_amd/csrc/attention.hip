@@ -65,15 +65,20 @@ __device__ __forceinline__ float sum8(f16x8 x, float acc) {
 
 // Column maxima of half-chunk scores s[nt] (s[nt][v] = score of key
 // 8(v/4) + 4half + v%4 of the half, query tile nt, column col) in log2 units
-// (`c` converts the scores to them).
+// (`c` converts the scores to them).  IEEE `maximum` (NaN-propagating) is
+// v_maximum3_f32, two scores per instruction with no canonicalising of the
+// MFMA results that fmaxf needs first (12 fewer VALU instructions per half
+// chunk at NT = 2).  A NaN score makes its column's output NaN either way: its
+// probability is NaN whatever the running max is.
 template <int NT>
 __device__ __forceinline__ void half_max(const f32x16 (&s)[NT], float c, float (&mx)[NT]) {
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
         float x = s[nt][0];
 #pragma unroll
-        for (int v = 1; v < 16; ++v) x = fmaxf(x, s[nt][v]);
-        mx[nt] = max_xor32(x) * c;
+        for (int v = 1; v < 16; ++v) x = __builtin_elementwise_maximum(x, s[nt][v]);
+        const float2 p = pair_xor32(x);
+        mx[nt] = __builtin_elementwise_maximum(p.x, p.y) * c;
     }
 }
 
@@ -81,22 +86,29 @@ __device__ __forceinline__ void half_max(const f32x16 (&s)[NT], float c, float (
 // max only moves when a column's max exceeds it by kLazyRescale, so the O
 // rescale runs on the first half chunk and rarely after; probabilities stay
 // below 2^kLazyRescale.  `enable` false (scores past the last chunk) leaves
-// the state unchanged.
+// the state unchanged.  The running max m of a column is held as the two
+// values the per-half code uses, both set only when m moves: nm = -m (0 while
+// m = -inf: the exponent offset of the probabilities) and mth = m +
+// kLazyRescale (the threshold, -inf while m = -inf).  -nm is m exactly, so
+// every decision is the one m itself would give, and so is the factor
+// 2^(m - mx) < 2^-kLazyRescale of a finite m; while m = -inf, l and O are
+// still zero, and min(., 0) keeps the factor finite (no 0 * inf).
 template <int NT, int MD>
-__device__ __forceinline__ void rescale_to(const float (&mx)[NT], bool enable, float (&m)[NT], float (&l)[NT],
-                                          float (&lt)[NT], f32x16 (&o)[MD][NT]) {
+__device__ __forceinline__ void rescale_to(const float (&mx)[NT], bool enable, float (&nm)[NT], float (&mth)[NT],
+                                          float (&l)[NT], float (&lt)[NT], f32x16 (&o)[MD][NT]) {
     bool need[NT];
     bool any_need = false;
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-        need[nt] = enable && mx[nt] > m[nt] + kLazyRescale;
+        need[nt] = enable && mx[nt] > mth[nt];
         any_need = any_need || need[nt];
     }
     if (__any(any_need)) {
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
-            const float alpha = need[nt] ? __builtin_amdgcn_exp2f(m[nt] - mx[nt]) : 1.0f;
-            m[nt] = need[nt] ? mx[nt] : m[nt];
+            const float alpha = need[nt] ? __builtin_amdgcn_exp2f(fminf(-nm[nt] - mx[nt], 0.0f)) : 1.0f;
+            nm[nt] = need[nt] ? -mx[nt] : nm[nt];
+            mth[nt] = need[nt] ? mx[nt] + kLazyRescale : mth[nt];
             l[nt] *= alpha;
             lt[nt] *= alpha;
 #pragma unroll
@@ -112,11 +124,11 @@ __device__ __forceinline__ void rescale_to(const float (&mx)[NT], bool enable, f
 // order), and their masses: l (and lt for tail chunks) sum the rounded
 // probabilities the PV product uses, so every output row's weights sum to 1.
 template <typename T, int NT>
-__device__ __forceinline__ void probs_half(const f32x16 (&s)[NT], float c, const float (&m)[NT], float (&l)[NT],
+__device__ __forceinline__ void probs_half(const f32x16 (&s)[NT], float c, const float (&nm)[NT], float (&l)[NT],
                                            float (&lt)[NT], bool tail, typename Elem<T>::vec8 (&pf)[NT][2]) {
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-        const float neg_m = (m[nt] == -__builtin_inff()) ? 0.0f : -m[nt];
+        const float neg_m = nm[nt];
         float rs = 0.0f;
 #pragma unroll
         for (int ss = 0; ss < 2; ++ss) {
@@ -127,7 +139,7 @@ __device__ __forceinline__ void probs_half(const f32x16 (&s)[NT], float c, const
             rs = sum8(p, rs);
         }
         l[nt] += rs;
-        lt[nt] += tail ? rs : 0.0f;
+        lt[nt] = tail ? lt[nt] + rs : lt[nt];  // (lt + 0 is not lt for lt = -0, so it would stay an add)
     }
 }
 
@@ -195,8 +207,18 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
     for (int nt = 0; nt < NT; ++nt) q_off[nt] = a.qmap.intra_offset(32 * (sub + nt) + col);
 
     // ---- query rows: qreg[nt][t] = Q[row nt][t*16+half*8 .. +7] (zero past
-    // the real head dim), kept in registers for the whole kernel
+    // the real head dim), kept in registers for the whole kernel.  At D = 256
+    // (QLDS) the fragments go to this wave's LDS (`lds`, 16 KB, fragment t at
+    // byte 1024 t, lane l's 16 bytes at 16 l) and each score MFMA reads its
+    // fragment there: with 64 registers of query fragments the kernel needs
+    // more than 512 registers and spills, and the register allocator has
+    // rebuilt a spilled fragment wrongly inside the chunk loop (one of its four
+    // dwords taken from the previous iteration's scores).
+    constexpr bool QLDS = D > 192 && !PERSIST;
     vec8 qreg[NT][KT];
+    auto q_lds = [&](int t) {
+        return reinterpret_cast<__attribute__((address_space(3))) u32x4*>(lds + t * 1024 + lane * 16);
+    };
     if (PERSIST && from_lds) {
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt)
@@ -220,14 +242,26 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
 #pragma unroll
                     for (int e = 0; e < 8; ++e) qreg[nt][t][e] = T(0.0f);
                 }
+                if constexpr (QLDS) *q_lds(t) = __builtin_bit_cast(u32x4, qreg[nt][t]);
             }
         }
     }
+    // query fragment t of tile nt for the score MFMAs; `qoff` is this lane's
+    // byte offset lane * 16, passed through an empty asm once per half chunk so
+    // that the LDS reads stay inside the chunk loop (hoisted out of it, they
+    // would hold the fragments in registers again)
+    auto qfrag = [&](int nt, int t, uint32_t qoff) -> vec8 {
+        if constexpr (QLDS)
+            return __builtin_bit_cast(
+                vec8, *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(lds + t * 1024 + qoff));
+        return qreg[nt][t];
+    };
     // Pins the query fragments to AGPRs (an empty asm with an "a" operand):
     // the architectural VGPRs hold O, S and P, and leaving the choice to the
     // register allocator makes it copy fragments between the two files.
     // MFMA reads its B operand from AGPRs directly.
     auto pin_q = [&]() {
+        if constexpr (QLDS) return;
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
@@ -245,10 +279,11 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
         for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
             for (int v = 0; v < 16; ++v) o[md][nt][v] = 0.0f;
-    float m[NT], l[NT], lt[NT];
+    float nm[NT], mth[NT], l[NT], lt[NT];  // running max as -m and m + kLazyRescale (rescale_to)
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-        m[nt] = -__builtin_inff();
+        nm[nt] = 0.0f;
+        mth[nt] = -__builtin_inff();
         l[nt] = 0.0f;
         lt[nt] = 0.0f;
     }
@@ -350,6 +385,8 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
             for (int ss = 0; ss < 2; ++ss) vf[md][2 * mt + ss] = ld_frag(p, md * 4 + 2 * mt + ss);
     };
     auto scores_half = [&](const vec8 (&k)[KT], f32x16 (&s)[NT]) {
+        uint32_t qoff = lane * 16;
+        if constexpr (QLDS) asm volatile("" : "+v"(qoff));
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
@@ -357,7 +394,7 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
 #pragma unroll
         for (int t = 0; t < KT; ++t)
 #pragma unroll
-            for (int nt = 0; nt < NT; ++nt) s[nt] = mfma32(k[t], qreg[nt][t], s[nt]);
+            for (int nt = 0; nt < NT; ++nt) s[nt] = mfma32(k[t], qfrag(nt, t, qoff), s[nt]);
     };
     auto pv_half = [&](int mt, const vec8 (&pf)[NT][2]) {
 #pragma unroll
@@ -441,7 +478,7 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
                 half_max<NT>(s, f, mx);
             }
         }
-        rescale_to<NT, MD>(mx, enable, m, l, lt, o);
+        rescale_to<NT, MD>(mx, enable, nm, mth, l, lt, o);
         return f;
     };
 
@@ -510,7 +547,7 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
 
             // ---- first half: scores in sa (issued, masked and max-checked one half earlier)
             if (!half0_only) scores_half(kf[1], sb);
-            probs_half<T, NT>(sa, ca, m, l, lt, tail, pf);
+            probs_half<T, NT>(sa, ca, nm, l, lt, tail, pf);
             load_k_half(kf[1], kn, 1);
             pv_half(0, pf);
             load_v_half(vn, 0);
@@ -518,7 +555,7 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
 
             // ---- second half: scores in sb; also scores the next chunk's first half
             if (!last) scores_half(kf[0], sa);
-            if (!half0_only) probs_half<T, NT>(sb, cb, m, l, lt, tail, pf);
+            if (!half0_only) probs_half<T, NT>(sb, cb, nm, l, lt, tail, pf);
             load_k_half(kf[0], kn2, 0);
             if (!half0_only) pv_half(1, pf);
             load_v_half(vn, 1);
@@ -664,8 +701,13 @@ void attention_kernel(AttnArgs a, const int32_t* __restrict__ sel, const uint32_
     const int work = xcd_remap(blockIdx.x, gridDim.x);
     const int block_work = work / SUBS;
     const int bh = block_work / a.q_blocks;
+    lds_char* qbuf = nullptr;
+    if constexpr (D > 192) {  // the query fragments of the wave (attention_block, QLDS)
+        __shared__ __attribute__((aligned(1024))) char q_lds[D / 16 * 1024];
+        qbuf = (lds_char*)q_lds;
+    }
     attention_block<T, D, NT, SPARSE, TAIL>(a, bh, block_work - bh * a.q_blocks, work - block_work * SUBS, sel,
-                                            selmask);
+                                            selmask, qbuf);
 }
 
 // Persistent variant (D = 128, head dim 128, a grid that splits evenly into the
