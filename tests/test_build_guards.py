@@ -13,9 +13,15 @@ change could break without any test of the outputs noticing at once:
   overwritten between the ``s_mov_b32 m0`` and the load);
 * every copy must be issued right after its ``s_mov_b32 m0``.
 
+A fourth guard: no kernel may spill vector registers to scratch.  The
+attention kernels run at up to 512 registers per lane; when one spilled, the
+register allocator rebuilt a spilled query fragment inside the chunk loop
+with one of its four dwords taken from the previous iteration's scores (the
+head-dim 256 kernel, whose query fragments now live in LDS instead).
+
 These tests compile the sources to gfx950 assembly with the library's own
-flags (about half a minute) and fail with the offending lines if any of this
-stops holding.
+flags (about a minute) and fail with the offending lines if any of this stops
+holding.
 """
 from __future__ import annotations
 
@@ -79,8 +85,29 @@ def test_wait_immediates_assemble_to_the_waits_they_name(tmp_path):
     assert lgkm0 == ["s_waitcnt lgkmcnt(0)"], lgkm0
 
 
-def test_only_the_lds_copies_use_m0(tmp_path):
-    kernels = _kernels(_device_asm(PKG / "csrc" / "attention.hip", tmp_path / "attention.s"))
+@pytest.fixture(scope="module")
+def device_asm(tmp_path_factory):
+    """gfx950 assembly of every kernel source of the library, by file name."""
+    out = tmp_path_factory.mktemp("asm")
+    return {src.name: _device_asm(src, out / (src.stem + ".s")) for src in sorted((PKG / "csrc").glob("*.hip"))}
+
+
+def test_no_kernel_spills_vector_registers(device_asm):
+    spills, checked = [], 0
+    for name, asm in device_asm.items():
+        if "amdhsa.kernels:" not in asm:  # host-only source (api.hip)
+            continue
+        entries = asm.split("amdhsa.kernels:", 1)[1]
+        for kernel, count in re.findall(r"\.name:\s+(\S+)[^-]*?\.vgpr_spill_count:\s+(\d+)", entries, re.S):
+            checked += 1
+            if int(count):
+                spills.append(f"{name}: {kernel} spills {count} registers")
+    assert checked >= 40, f"kernel metadata of only {checked} kernels found"
+    assert not spills, "\n".join(spills)
+
+
+def test_only_the_lds_copies_use_m0(device_asm):
+    kernels = _kernels(device_asm["attention.hip"])
     persistent = {n: b for n, b in kernels.items() if "attention_persistent_kernel" in n}
     assert persistent, "no persistent attention kernel in attention.hip"
     copies = 0
