@@ -70,15 +70,30 @@ __device__ __forceinline__ float sum8(f16x8 x, float acc) {
 // MFMA results that fmaxf needs first (12 fewer VALU instructions per half
 // chunk at NT = 2).  A NaN score makes its column's output NaN either way: its
 // probability is NaN whatever the running max is.
+// With two tiles, one swap of the lanes' partial maxima leaves lanes 0-31 with
+// both halves' values of tile 0 and lanes 32-63 with those of tile 1; their
+// maximum, swapped with itself, gives every lane both column maxima.
 template <int NT>
 __device__ __forceinline__ void half_max(const f32x16 (&s)[NT], float c, float (&mx)[NT]) {
+    float x[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-        float x = s[nt][0];
+        x[nt] = s[nt][0];
 #pragma unroll
-        for (int v = 1; v < 16; ++v) x = __builtin_elementwise_maximum(x, s[nt][v]);
-        const float2 p = pair_xor32(x);
-        mx[nt] = __builtin_elementwise_maximum(p.x, p.y) * c;
+        for (int v = 1; v < 16; ++v) x[nt] = __builtin_elementwise_maximum(x[nt], s[nt][v]);
+    }
+    if constexpr (NT == 2) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x[0]), __float_as_uint(x[1]), false, false);
+        const float both = __builtin_elementwise_maximum(__uint_as_float(r[0]), __uint_as_float(r[1]));
+        const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(both), __float_as_uint(both), false, false);
+        mx[0] = __uint_as_float(b[0]) * c;
+        mx[1] = __uint_as_float(b[1]) * c;
+    } else {
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            const float2 p = pair_xor32(x[nt]);
+            mx[nt] = __builtin_elementwise_maximum(p.x, p.y) * c;
+        }
     }
 }
 
@@ -123,13 +138,15 @@ __device__ __forceinline__ void rescale_to(const float (&mx)[NT], bool enable, f
 // 16ss .. 16ss+15 of the half in swap23 order, which is the accumulator row
 // order), and their masses: l (and lt for tail chunks) sum the rounded
 // probabilities the PV product uses, so every output row's weights sum to 1.
+// Exact chunks accumulate straight into l; tail chunks form the half's sum
+// first, which goes to both l and lt.
 template <typename T, int NT>
 __device__ __forceinline__ void probs_half(const f32x16 (&s)[NT], float c, const float (&nm)[NT], float (&l)[NT],
                                            float (&lt)[NT], bool tail, typename Elem<T>::vec8 (&pf)[NT][2]) {
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
         const float neg_m = nm[nt];
-        float rs = 0.0f;
+        float rs = tail ? 0.0f : l[nt];
 #pragma unroll
         for (int ss = 0; ss < 2; ++ss) {
             typename Elem<T>::vec8 p;
@@ -138,8 +155,8 @@ __device__ __forceinline__ void probs_half(const f32x16 (&s)[NT], float c, const
             pf[nt][ss] = p;
             rs = sum8(p, rs);
         }
-        l[nt] += rs;
-        lt[nt] = tail ? lt[nt] + rs : lt[nt];  // (lt + 0 is not lt for lt = -0, so it would stay an add)
+        l[nt] = tail ? l[nt] + rs : rs;
+        lt[nt] = tail ? lt[nt] + rs : lt[nt];
     }
 }
 
