@@ -633,6 +633,11 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
         }
     }
     typedef T vec4 __attribute__((ext_vector_type(4)));
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    // 16-byte stores when every output row start is 16-byte aligned (8-byte
+    // ones otherwise)
+    const bool st16 = (reinterpret_cast<uintptr_t>(a.o.data) % 16 == 0) &&
+                      ((a.o.sb | a.o.sh | a.o.st) * (int64_t)sizeof(T)) % 16 == 0;
 #pragma unroll
     for (int md = 0; md < MD; ++md) {
         f32x16 corr[NT];
@@ -654,11 +659,11 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
         }
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
-            if (!ovalid[nt]) continue;
+            if (!ovalid[nt]) continue;  // lanes l and l + 32 (one query) take the same branch
+            // w[g]: the 4 outputs of accumulator group g packed, dims 8g + 4half ..
+            u32x2 w[4];
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-                const int d = md * 32 + 8 * g + 4 * half;
-                if (!all_dims && d >= a.head_dim) continue;
                 vec4 out;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
@@ -666,7 +671,30 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
                     if (first_order) x += corr[nt][4 * g + e] * wa[nt];
                     out[e] = from_f32<T>(x);
                 }
-                *reinterpret_cast<vec4*>(obase[nt] + d * sizeof(T)) = out;
+                w[g] = __builtin_bit_cast(u32x2, out);
+            }
+            if (st16) {
+                // one lane-half swap per dword of groups 2p and 2p + 1 leaves lanes
+                // 0-31 with dims 8(2p) .. +7 of their query and lanes 32-63 with
+                // dims 8(2p + 1) .. +7: one 16-byte store each
+#pragma unroll
+                for (int p = 0; p < 2; ++p) {
+                    u32x4 x16;
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        const auto r = __builtin_amdgcn_permlane32_swap(w[2 * p][j], w[2 * p + 1][j], false, false);
+                        x16[j] = r[0];
+                        x16[2 + j] = r[1];
+                    }
+                    const int d = md * 32 + 8 * (2 * p + half);
+                    if (all_dims || d < a.head_dim) *reinterpret_cast<u32x4*>(obase[nt] + d * sizeof(T)) = x16;
+                }
+            } else {
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int d = md * 32 + 8 * g + 4 * half;
+                    if (all_dims || d < a.head_dim) *reinterpret_cast<u32x2*>(obase[nt] + d * sizeof(T)) = w[g];
+                }
             }
         }
     }
