@@ -385,8 +385,15 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
     };
     auto kptr = [&](int x, int row) { return Src{is_tail(x) ? kc_rs : kp_rs, row * (int)kBlockBytes}; };
     auto vptr = [&](int x, int row) { return Src{is_tail(x) ? vc_rs : vp_rs, row * (int)kBlockBytes}; };
+    // fragment `frag` of a chunk: the 4 KB-aligned part of its offset is scalar
+    // (wave-uniform, read from the first lane so that the compiler never treats
+    // it as a per-lane value), the rest (< 4 KB) a constant on the lane offset
+    // that the load's immediate offset field carries, so four consecutive
+    // fragments share one scalar offset
     auto ld_frag = [&](const Src& p, int frag) -> vec8 {
-        return __builtin_bit_cast(vec8, __builtin_amdgcn_raw_buffer_load_b128(p.rs, lane_off, p.off + frag * 1024, 0));
+        const int soff = __builtin_amdgcn_readfirstlane(p.off + (frag >> 2) * 4096);
+        return __builtin_bit_cast(vec8,
+                                  __builtin_amdgcn_raw_buffer_load_b128(p.rs, lane_off + (frag & 3) * 1024, soff, 0));
     };
 
     vec8 kf[2][KT];   // kf[mt]: key fragments of the next half chunk that uses them
