@@ -21,7 +21,7 @@ BUILD_DIR = PACKAGE_DIR / "_build"
 LIB_PATH = PACKAGE_DIR / "mi355x_pisa" / "libpisa_hip.so"
 ARCH = "gfx950"
 
-SOURCES = ("api.hip", "stats.hip", "route.hip", "attention.hip", "fixed_block.hip", "layout.hip")
+SOURCES = ("api.hip", "stats.hip", "route.hip", "attention.hip", "attention_dense.hip", "fixed_block.hip", "layout.hip")
 
 COMMON_FLAGS = [
     f"--offload-arch={ARCH}",
@@ -48,6 +48,17 @@ COMMON_FLAGS = [
 ]
 
 
+# Per-source additions: the dense attention kernels (attention_dense.hip) are
+# scheduled by LLVM's max-memory-clause strategy, which measured 1.6 % faster
+# on them than the default and slower on the sparse kernels.
+EXTRA_FLAGS = {"attention_dense.hip": ["-mllvm", "-amdgpu-sched-strategy=max-memory-clause"]}
+
+
+def flags_for(name: str) -> list[str]:
+    """Compiler flags of one source file of csrc/."""
+    return [*COMMON_FLAGS, *EXTRA_FLAGS.get(name, [])]
+
+
 def _hipcc() -> str:
     for candidate in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
         if candidate and pathlib.Path(candidate).exists():
@@ -69,7 +80,7 @@ def build(jobs: int | None = None) -> pathlib.Path:
     hipcc = _hipcc()
     BUILD_DIR.mkdir(exist_ok=True)
     objects = [BUILD_DIR / (name.rsplit(".", 1)[0] + ".o") for name in SOURCES]
-    commands = [[hipcc, *COMMON_FLAGS, "-c", str(CSRC / name), "-o", str(obj)] for name, obj in zip(SOURCES, objects)]
+    commands = [[hipcc, *flags_for(name), "-c", str(CSRC / name), "-o", str(obj)] for name, obj in zip(SOURCES, objects)]
     workers = jobs or min(len(commands), max(1, min(8, os.cpu_count() or 1)))
     with concurrent.futures.ThreadPoolExecutor(max_workers=workers) as pool:
         for future in [pool.submit(_run, cmd) for cmd in commands]:

@@ -915,6 +915,24 @@ int launch_attention_t(const AttnArgs& a_in, int bh_count, hipStream_t stream) {
     return pisa_host::check_launch("attention_kernel");
 }
 
+// The dense launchers (SPARSE = TAIL = false) are compiled in a translation
+// unit of their own, attention_dense.hip (this file with PISA_ATTENTION_DENSE
+// defined), under the max-memory-clause machine scheduler: it serves the dense
+// chunk loop better and the sparse one worse.  This file without the macro
+// holds the sparse kernels, the dispatcher and the packing kernel.
+#define PISA_DENSE_INSTANCES(X) \
+    X(bf16_t, 64) X(bf16_t, 96) X(bf16_t, 128) X(bf16_t, 160) X(bf16_t, 192) X(bf16_t, 256) \
+    X(f16_t, 64) X(f16_t, 96) X(f16_t, 128) X(f16_t, 160) X(f16_t, 192) X(f16_t, 256)
+#ifdef PISA_ATTENTION_DENSE
+#define PISA_DENSE_INSTANCE(T, D) template int launch_attention_t<T, D, false, false>(const AttnArgs&, int, hipStream_t);
+PISA_DENSE_INSTANCES(PISA_DENSE_INSTANCE)
+#undef PISA_DENSE_INSTANCE
+#else
+#define PISA_DENSE_EXTERN(T, D) \
+    extern template int launch_attention_t<T, D, false, false>(const AttnArgs&, int, hipStream_t);
+PISA_DENSE_INSTANCES(PISA_DENSE_EXTERN)
+#undef PISA_DENSE_EXTERN
+
 template <typename T, int D>
 int launch_attention_d(bool sparse, bool tail, const AttnArgs& a, int bh_count, hipStream_t stream) {
     if (sparse && tail) return launch_attention_t<T, D, true, true>(a, bh_count, stream);
@@ -969,5 +987,6 @@ int launch_kv_pack(int dtype, int padded, int head_dim, const View& k, const Vie
         return launch_kv_pack_t<bf16_t>(padded, head_dim, k, v, map, kv_tokens, kv_blocks, bh_count, kp, vp, stream);
     return launch_kv_pack_t<f16_t>(padded, head_dim, k, v, map, kv_tokens, kv_blocks, bh_count, kp, vp, stream);
 }
+#endif  // PISA_ATTENTION_DENSE
 
 }  // namespace pisa

@@ -44,7 +44,7 @@ pytestmark = pytest.mark.skipif(HIPCC is None, reason="hipcc is not installed")
 
 
 def _device_asm(source: pathlib.Path, out: pathlib.Path) -> str:
-    cmd = [HIPCC, *build_lib.COMMON_FLAGS, f"-I{PKG / 'csrc'}", "-S", "--cuda-device-only", str(source),
+    cmd = [HIPCC, *build_lib.flags_for(source.name), f"-I{PKG / 'csrc'}", "-S", "--cuda-device-only", str(source),
            "-o", str(out)]
     result = subprocess.run(cmd, capture_output=True, text=True)
     assert result.returncode == 0, result.stderr[-2000:]
@@ -107,7 +107,7 @@ def test_no_kernel_spills_vector_registers(device_asm):
 
 
 def test_only_the_lds_copies_use_m0(device_asm):
-    kernels = _kernels(device_asm["attention.hip"])
+    kernels = {**_kernels(device_asm["attention.hip"]), **_kernels(device_asm["attention_dense.hip"])}
     persistent = {n: b for n, b in kernels.items() if "attention_persistent_kernel" in n}
     assert persistent, "no persistent attention kernel in attention.hip"
     copies = 0
