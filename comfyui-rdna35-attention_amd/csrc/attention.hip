@@ -160,9 +160,9 @@ __device__ __forceinline__ void probs_half(const f32x16 (&s)[NT], float c, const
     }
 }
 
-// The block a persistent wave runs next (nt = 0: none): its query rows and the
-// key and value fragments of its first chunk are copied to the wave's LDS
-// while the current block runs.
+// The block a persistent wave runs next (nt = 0: none): its query rows (and,
+// in the dense kernel, its first chunk) are copied to the wave's LDS while the
+// current block runs.
 // Chunk-step kinds of the attention loop (see check_half / chunk_step).
 constexpr int kStepGeneral = 0, kStepExact = 1, kStepTail = 2;
 
@@ -332,11 +332,15 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
     const __amdgpu_buffer_rsrc_t ht_rs = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(first_order ? a.ht + (int64_t)bh * D * D * sizeof(T) : a.kp), (short)0,
         first_order ? D * D * (int)sizeof(T) : 0, kRawFlags);
-    // Copies the next block's query rows (fragment nt*KT + t at 1 KB each), the
-    // key fragments of its first chunk (LDS + 16 KB) and the value fragments of
-    // that chunk's first half (LDS + 32 KB) to this wave's LDS.
-    const int next_row0 = (PERSIST && SPARSE && next.nt > 0 && n_exact > 0)
-                              ? sel[((int64_t)next.bh * a.q_blocks + next.qb) * a.exact] : 0;
+    // Copies the next block's query rows (fragment nt*KT + t at 1 KB each) to
+    // this wave's LDS, and in the dense kernel (kCopyChunk) also the key
+    // fragments of its first chunk (LDS + 16 KB) and the value fragments of that
+    // chunk's first half (LDS + 32 KB).  The query rows come from the raster
+    // layout in HBM; a sparse block's first chunk is usually an L2 hit, and
+    // each copy waits for room in the CU's memory queue, so copying it made
+    // the sparse kernel slower (dense blocks all start at the same chunk, which
+    // gains from the copy a little).
+    constexpr bool kCopyChunk = !SPARSE;
     auto prefetch_next = [&]() {
         if (!PERSIST || next.nt == 0) return;
         __builtin_amdgcn_s_waitcnt(kWaitLgkm0);  // this block's LDS reads have landed
@@ -352,17 +356,11 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
                 for (int t = 0; t < KT; ++t) lds_copy16(p + t * 32, lds_addr + (nt * KT + t) * 1024);
             }
         }
-        if (n_chunks > 0) {
-            const bool tail0 = TAIL && n_exact == 0;
-            const int row = tail0 ? 0 : min(max(next_row0, 0), a.kv_blocks - 1);
-            const char* src = (tail0 ? a.kbar + (int64_t)next.bh * a.npad * D * sizeof(T)
-                                     : a.kp + (int64_t)next.bh * a.kv_blocks * kBlockBytes) +
-                              (int64_t)row * kBlockBytes + lane_off;
+        if (kCopyChunk && n_chunks > 0) {
+            const char* src = a.kp + (int64_t)next.bh * a.kv_blocks * kBlockBytes + lane_off;
 #pragma unroll
             for (int f = 0; f < 2 * KT; ++f) lds_copy16(src + f * 1024, lds_addr + 16384 + f * 1024);
-            const char* vsrc = (tail0 ? a.vbar_t + (int64_t)next.bh * a.npad * D * sizeof(T)
-                                      : a.vp + (int64_t)next.bh * a.kv_blocks * kBlockBytes) +
-                               (int64_t)row * kBlockBytes + lane_off;
+            const char* vsrc = a.vp + (int64_t)next.bh * a.kv_blocks * kBlockBytes + lane_off;
 #pragma unroll
             for (int md = 0; md < MD; ++md)
 #pragma unroll
@@ -519,17 +517,12 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
         // at the loop head cover just the chunk loads in flight.  The loads
         // after the first scores go out in the loop's order (K half 1, V half
         // 0, next K half 0, V half 1).
-        if (PERSIST && from_lds) {
+        if (kCopyChunk && PERSIST && from_lds) {
 #pragma unroll
             for (int f = 0; f < 2 * KT; ++f)
                 kf[f / KT][f % KT] = __builtin_bit_cast(
                     vec8, *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(
                               lds + 16384 + f * 1024 + lane * 16));
-        } else {
-            load_k_half(kf[0], k0, 0);
-            load_k_half(kf[1], k0, 1);
-        }
-        if (PERSIST && from_lds) {
 #pragma unroll
             for (int md = 0; md < MD; ++md)
 #pragma unroll
@@ -538,6 +531,8 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
                         vec8, *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(
                                   lds + 32768 + (md * 2 + ss) * 1024 + lane * 16));
         } else {
+            load_k_half(kf[0], k0, 0);
+            load_k_half(kf[1], k0, 1);
             load_v_half(v0, 0);
         }
         pin_q();
@@ -606,7 +601,7 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
         chunk_step(cl, true, TAIL && is_tail(cl) && table_row(cl) * kBlock + 32 >= a.centroids, kStepGeneral);
     }
 
-    // The copies of the next block's query rows and first chunk go out here,
+    // The copies of the next block's query rows go out here,
     // after an explicit wait for this block's last loads (the correction's
     // fragments, needed next anyway): the copies are hidden from the compiler's
     // counters, so every wait issued after them also waits for them.  Issued in
@@ -768,14 +763,14 @@ void attention_kernel(AttnArgs a, const int32_t* __restrict__ sel, const uint32_
 // it < F = qx / S, then its share of the r = qx mod S blocks left: one-tile
 // halves of block x*qx + F*S + j/2 when 2r <= S (as attention_kernel's split),
 // else whole block x*qx + F*S + j for j < r.  While a block runs, the next
-// block's query rows and first chunk are copied to the wave's LDS (40 KB per
-// wave, 160 KB per CU; direct-to-LDS loads), so its prologue reads LDS instead
-// of waiting on HBM.
+// block's query rows (and in the dense kernel its first chunk) are copied to
+// the wave's LDS (16 KB, dense 40 KB per wave; direct-to-LDS loads), so its
+// prologue reads them from LDS instead of waiting on HBM.
 template <typename T, bool SPARSE, bool TAIL>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void attention_persistent_kernel(AttnArgs a, const int32_t* __restrict__ sel, const uint32_t* __restrict__ selmask) {
     constexpr int D = 128;
-    __shared__ __attribute__((aligned(1024))) char lds_buf[40 * 1024];
+    __shared__ __attribute__((aligned(1024))) char lds_buf[(SPARSE ? 16 : 40) * 1024];
     lds_char* const lds = (lds_char*)lds_buf;
     const int xcd = blockIdx.x & 7;
     const int j = blockIdx.x >> 3;
