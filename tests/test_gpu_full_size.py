@@ -181,6 +181,23 @@ def test_c5_video_selection_and_one_head(native):
     assert equal.mean() >= 0.99
 
 
+def test_max_size_video_pisa_matches_oracle(native):
+    """T = 65536, the largest sequence the native path takes (1024 blocks): routing over 1024 candidates per row
+    (16 per lane in the selection), 16 centroid chunks in the attention tail; one head against the oracle."""
+    from mi355x_pisa.synthetic import video_qkv
+
+    grid = (16, 64, 64)
+    q, k, v = video_qkv(batch=1, heads=2, grid=grid, seed=11, device="cuda")
+    exact = 16
+    out, scores, idx = native.forward_with_routing(q, k, v, exact, D ** -0.5, hyd=False, token_grid=grid)
+    assert scores.shape == (2, 1024, 1024) and idx.shape == (2, 1024, exact)
+    assert torch.isfinite(out).all()
+    np.testing.assert_array_equal(idx.cpu().numpy(), opisa.topk_ascending(np32(scores), exact))
+    packed = [spatial_to_packed(t[:, 1:2], *grid) for t in (q, k, v)]
+    expected = packed_to_merged(opisa.generic_forward(*packed, exact, dtype="bf16"), 1, 1, *grid)
+    assert_close(np32(out[0, 1]), expected[0], 5e-2, 5e-2, "T=65536 head 1")
+
+
 @pytest.mark.parametrize("grid", [(2, 64, 64), (1, 64, 128), (8, 32, 32)])
 def test_wan_ltx_t8192_generic_routes_on_hyd_statistics(native, grid):
     """Generic PISA at T = 8192, D = 128, bf16 (the Wan/LTX regime of README.md:110-112): the
