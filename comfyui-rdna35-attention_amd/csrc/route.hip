@@ -1,14 +1,17 @@
 // HYD and centroid routing scores and per-query-block top-k selection.
 //
-// One 256-thread workgroup owns 16 routing rows (query blocks i) of one
+// One 256-thread workgroup owns 16 (or 8) routing rows (query blocks i) of one
 // (batch, head).  Scores S[i][j] = q_i . k_j for every key block j are 16 x 16
 // tiles of MFMA written to LDS: for HYD with bf16 inputs the bf16 means the
 // statistics kernel wrote (which equal the bf16 rounding of the fp32 means) on
 // v_mfma_f32_16x16x32_bf16, otherwise the fp32 means on v_mfma_f32_16x16x4_f32
 // (rounded to bf16 first for HYD); every product is exact and only the fp32
-// summation order is the hardware's.  Then each wave selects 4 rows: lane l
-// holds the candidates j = l, l+64, ... of a row (scale, HYD bias
-// ln(h_norm + 1e-5), sink override +inf).
+// summation order is the hardware's.  Then each wave selects 4 (or 2) rows:
+// lane l holds the candidates j = l, l+64, ... of a row (scale, HYD bias
+// ln(h_norm + 1e-5), sink override +inf).  The launch is a chain of dependent
+// loads, products and ballot rounds per workgroup; when 16-row workgroups
+// would leave the CUs with fewer than two each, 8-row workgroups (half of
+// each score tile unused) halve the selection and store part of that chain.
 //
 // With head dim 128 the same launch also carries the H_sum reduction
 // (reduce_h_tile): workgroups past the routing ones each sum two 32x32 tiles,
@@ -19,8 +22,8 @@
 // selected, and keys equal to T are taken in ascending block order until k
 // are chosen - i.e. the k largest scores with ties to the lowest index,
 // independent of scheduling, so the selection is reproducible bit for bit.
-// Four rows are searched together, with no branch between them, until every
-// row's prefix has exactly k keys at or above it.  Indices are written in
+// A wave's rows are searched together, with no branch between them, until
+// every row's prefix has exactly k keys at or above it.  Indices are written in
 // ascending order, with the selection bit mask the attention tail uses (lane w
 // writing word w).  h_norm is loaded before the scores are formed.
 //
@@ -32,8 +35,7 @@
 namespace pisa {
 
 constexpr int kRouteWaves = 4;
-constexpr int kRouteTile = 16;  // routing rows per workgroup
-constexpr int kRouteRows = 4;   // rows selected together per wave
+constexpr int kScoreRows = 16;  // rows of a score tile (rows of the 16x16 MFMA tiles)
 
 __device__ __forceinline__ uint32_t order_key(float x) {
     uint32_t b = __float_as_uint(x);
@@ -50,19 +52,23 @@ __device__ __forceinline__ f32x4 mfma16_f32(float a, float b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
-// One 256-thread workgroup owns kRouteTile = 16 routing rows of one head.
+// One 256-thread workgroup owns TILE (16 or 8) routing rows of one head.
 // Scores: each wave takes every 4th 16-candidate tile and forms the 16 x 16
 // tile S[i][j] = sum_d q_i[d] k_j[d] with fp32 16x16x4 MFMAs (the four lane
 // groups take interleaved groups of 4 dims, so each lane loads aligned 16-byte
 // pieces of one query row and one key row, the next 16 steps' pieces in
 // flight while the current ones are multiplied); products of the
 // (bf16-rounded for HYD) fp32 inputs are exact, sums are fp32.  The tile goes
-// to LDS.  Selection: wave w takes rows 4w .. 4w+3 together, lane l reading
-// candidates l, l+64, ... of a row from LDS.  T: dtype of the H_sum copy of
-// the fused reduction workgroups.
-template <int PL, typename T>  // candidates per lane in the selection: N <= 64 * PL
+// to LDS (rows past TILE are formed and not used).  Selection: wave w takes
+// rows TILE/4 w .. TILE/4 (w+1) - 1 together, lane l reading candidates l,
+// l+64, ... of a row from LDS.  T: dtype of the H_sum copy of the fused
+// reduction workgroups.
+template <int PL, int TILE, typename T>  // candidates per lane in the selection: N <= 64 * PL
 __global__ __launch_bounds__(64 * kRouteWaves) void route_topk_kernel(RouteArgs a, ReduceArgs r, int fuse_reduce) {
-    extern __shared__ __attribute__((aligned(16))) float s_lds[];  // [kRouteTile][N + 1]
+    static_assert(TILE == 16 || TILE == 8, "routing rows per workgroup");
+    constexpr int kRouteTile = TILE;
+    constexpr int kRouteRows = TILE / kRouteWaves;  // rows selected together per wave
+    extern __shared__ __attribute__((aligned(16))) float s_lds[];  // [kScoreRows][N + 1]
     __shared__ float red_tile[32][33];
     const int t = threadIdx.x;
     const int lane = t & 63;
@@ -225,7 +231,7 @@ __global__ __launch_bounds__(64 * kRouteWaves) void route_topk_kernel(RouteArgs 
     const uint64_t lt_mask = (1ull << lane) - 1ull;
     const int k = a.k;
     {
-        const int r0 = kRouteRows * wave;  // local rows r0 .. r0+3
+        const int r0 = kRouteRows * wave;  // local rows r0 .. r0 + kRouteRows - 1
         uint32_t key[kRouteRows][PL];
 #pragma unroll
         for (int rr = 0; rr < kRouteRows; ++rr) {
@@ -305,14 +311,14 @@ __global__ __launch_bounds__(64 * kRouteWaves) void route_topk_kernel(RouteArgs 
     }
 }
 
-template <int PL, typename T>
+template <int PL, int TILE, typename T>
 static int launch_route_pl(const RouteArgs& a, const ReduceArgs& r, int fuse, hipStream_t stream) {
-    const int row_tiles = (a.blocks + kRouteTile - 1) / kRouteTile;
+    const int row_tiles = (a.blocks + TILE - 1) / TILE;
     const int bh_count = a.rows / a.blocks;
     const dim3 grid(bh_count * row_tiles + (fuse ? bh_count * 8 : 0));  // routing, then reduction workgroups
     // dynamic LDS: 16 score rows of N + 1 floats (65.6 KB at N = 1024, beside
     // 4.2 KB of static LDS); gfx950 has 160 KB per workgroup, checked here
-    const size_t lds = (size_t)kRouteTile * (a.blocks + 1) * sizeof(float);
+    const size_t lds = (size_t)kScoreRows * (a.blocks + 1) * sizeof(float);
     static const int lds_limit = [] {
         int dev = 0, bytes = 0;
         if (hipGetDevice(&dev) != hipSuccess ||
@@ -324,19 +330,34 @@ static int launch_route_pl(const RouteArgs& a, const ReduceArgs& r, int fuse, hi
     if (lds_limit <= 0 || lds + static_lds > (size_t)lds_limit)
         return pisa_host::fail(PISA_ERR_UNSUPPORTED, "routing over %d blocks needs %zu bytes of LDS, device allows %d",
                                a.blocks, lds + static_lds, lds_limit);
-    hipLaunchKernelGGL((route_topk_kernel<PL, T>), grid, dim3(64 * kRouteWaves), lds, stream, a, r, fuse);
+    hipLaunchKernelGGL((route_topk_kernel<PL, TILE, T>), grid, dim3(64 * kRouteWaves), lds, stream, a, r, fuse);
     return PISA_OK;
 }
 
+// 8-row workgroups when 16-row ones would give the CUs fewer than two each
+// (C4: 288 workgroups of 16 rows on 256 CUs; prepare 105.9 -> 103.5 us), and
+// only up to 256 candidates: every workgroup forms the score
+// tiles of all N candidates, so at C5 (N = 512, 1280 workgroups of 16 rows)
+// halving the rows per workgroup doubles that work and the launch is 65 us
+// slower.
 template <typename T>
 static int launch_route_t(const RouteArgs& a, const ReduceArgs& r, int fuse, hipStream_t stream) {
+    static const int cus = [] {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            return 0;
+        return n;
+    }();
     const int pl = (a.blocks + 63) / 64;
-    if (pl <= 1) return launch_route_pl<1, T>(a, r, fuse, stream);
-    if (pl <= 2) return launch_route_pl<2, T>(a, r, fuse, stream);
-    if (pl <= 3) return launch_route_pl<3, T>(a, r, fuse, stream);
-    if (pl <= 4) return launch_route_pl<4, T>(a, r, fuse, stream);
-    if (pl <= 8) return launch_route_pl<8, T>(a, r, fuse, stream);
-    return launch_route_pl<16, T>(a, r, fuse, stream);
+    const int64_t wgs16 = (int64_t)(a.rows / a.blocks) * ((a.blocks + 15) / 16);
+    const bool rows8 = pl <= 4 && wgs16 < 2 * (int64_t)cus;
+    if (pl <= 1) return rows8 ? launch_route_pl<1, 8, T>(a, r, fuse, stream) : launch_route_pl<1, 16, T>(a, r, fuse, stream);
+    if (pl <= 2) return rows8 ? launch_route_pl<2, 8, T>(a, r, fuse, stream) : launch_route_pl<2, 16, T>(a, r, fuse, stream);
+    if (pl <= 3) return rows8 ? launch_route_pl<3, 8, T>(a, r, fuse, stream) : launch_route_pl<3, 16, T>(a, r, fuse, stream);
+    if (pl <= 4) return rows8 ? launch_route_pl<4, 8, T>(a, r, fuse, stream) : launch_route_pl<4, 16, T>(a, r, fuse, stream);
+    if (pl <= 8) return launch_route_pl<8, 16, T>(a, r, fuse, stream);
+    return launch_route_pl<16, 16, T>(a, r, fuse, stream);
 }
 
 int launch_route(const RouteArgs& a, hipStream_t stream) {
