@@ -82,6 +82,23 @@ def test_c4_selection_agrees_with_the_oracle_on_every_head(native, anima):
     assert equal.mean() >= 0.99
 
 
+def test_c4_routing_row_tiling_does_not_change_bits(native, anima):
+    """C4 (32 heads) routes in workgroups of 8 query blocks, the same heads twice (64 heads, enough
+    workgroups to fill every CU twice) in workgroups of 16: each score is the same MFMA sum either way,
+    so scores and selections must be bit-identical.  The outputs agree to rounding only: the statistics
+    grid also depends on the head count (64 heads: 8 chunks of 18 blocks per head instead of 16 of 9),
+    and H_sum sums its chunk partials in a different grouping."""
+    q, k, v = anima
+    out, scores, idx = native.forward_with_routing(q, k, v, 23, D ** -0.5, token_grid=(1, 96, 96))
+    q2, k2, v2 = (torch.cat([t, t]) for t in (q, k, v))
+    out2, scores2, idx2 = native.forward_with_routing(q2, k2, v2, 23, D ** -0.5, token_grid=(1, 96, 96))
+    for half in (slice(0, 32), slice(32, 64)):
+        assert torch.equal(scores2[half], scores)
+        assert torch.equal(idx2[half], idx)
+    for part in (out2[:2], out2[2:]):
+        torch.testing.assert_close(part.float(), out.float(), atol=1e-2, rtol=1e-2)
+
+
 def test_c4_constant_values_are_exact(native, anima):
     q, k, _ = anima
     v = torch.full_like(q, 0.3125)  # exactly representable; any convex combination returns it
