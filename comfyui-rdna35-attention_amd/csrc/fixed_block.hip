@@ -330,14 +330,22 @@ __global__ __launch_bounds__(64) void fixed_block_mfma_kernel(View q, View k, Vi
 //     output tile m is dim VW*i + m (VW = D/16), so a lane reads VW
 //     consecutive dims of a key row with one load and, at the end, holds the
 //     4*VW consecutive dims 4*VW*g .. of its query.
-// Nothing is staged in LDS; rows past the block's length are read clamped to
-// its last row (unconditional loads, so the compiler's wait counts stay
-// partial) and get probability 0 (keys) or are not stored (queries).
+// The block's K and V rows are loaded once per workgroup (wave w reads rows
+// 16w .. 16w+15 of both) and staged in LDS with padded rows, from where every
+// wave reads its operands: with each wave loading all 64 rows itself, the four
+// waves moved four times the K/V bytes through the CU's memory path (C1:
+// 13.4 -> 11.3 us).  Q rows are read by their own wave.  Rows past the block's
+// length are read clamped to its last row (unconditional loads, so the
+// compiler's wait counts stay partial) and get probability 0 (keys) or are not
+// stored (queries).
 template <int D>
 __global__ __launch_bounds__(256) void fixed_block_f32_mfma_kernel(View q, View k, View v, OutView o, int tokens,
                                                                    int nblocks, float scale, int causal) {
     constexpr int S4 = D / 16;  // float4 pieces of a Q or K row per lane
     constexpr int VW = D / 16;  // V dims per lane per key row = output dim tiles
+    constexpr int kRowF = D + 4;  // padded LDS row (floats)
+    __shared__ __attribute__((aligned(16))) float ks[64 * kRowF];
+    __shared__ __attribute__((aligned(16))) float vs[64 * kRowF];
     const int lane = threadIdx.x & 63;
     const int w = threadIdx.x >> 6;
     const int c = lane & 15;
@@ -355,39 +363,45 @@ __global__ __launch_bounds__(256) void fixed_block_f32_mfma_kernel(View q, View 
 #pragma unroll
         for (int s4 = 0; s4 < S4; ++s4) qv[s4] = *reinterpret_cast<const f32x4*>(qr + 16 * s4 + 4 * g);
     }
-#pragma unroll
-    for (int n = 0; n < 4; ++n) {
-        const float* kr = at(k, 16 * n + c);
-#pragma unroll
-        for (int s4 = 0; s4 < S4; ++s4) kv[n][s4] = *reinterpret_cast<const f32x4*>(kr + 16 * s4 + 4 * g);
-    }
     float vv[4][4][VW];
+    {
+        // staging: lane l of wave w loads dims D/4 (l%4) .. of row 16w + l/4 of K and V
+        constexpr int P = D / 16;  // float4 pieces per lane
+        const int row = 16 * w + (lane >> 2);
+        const int d0 = (lane & 3) * (D / 4);
+        const float* kr = at(k, row) + d0;
+        const float* vr = at(v, row) + d0;
+        f32x4 xk[P], xv[P];
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+            xk[p] = *reinterpret_cast<const f32x4*>(kr + 4 * p);
+            xv[p] = *reinterpret_cast<const f32x4*>(vr + 4 * p);
+        }
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+            *reinterpret_cast<f32x4*>(&ks[row * kRowF + d0 + 4 * p]) = xk[p];
+            *reinterpret_cast<f32x4*>(&vs[row * kRowF + d0 + 4 * p]) = xv[p];
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int n = 0; n < 4; ++n)
+#pragma unroll
+        for (int s4 = 0; s4 < S4; ++s4)
+            kv[n][s4] = *reinterpret_cast<const f32x4*>(&ks[(16 * n + c) * kRowF + 16 * s4 + 4 * g]);
 #pragma unroll
     for (int n = 0; n < 4; ++n)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int key = 16 * n + 4 * g + r;
-            const float* vr = at(v, key) + VW * c;
-            if constexpr (VW == 2) {
-                const float2 x = *reinterpret_cast<const float2*>(vr);
-                vv[n][r][0] = x.x;
-                vv[n][r][1] = x.y;
-            } else {
 #pragma unroll
-                for (int j = 0; j < VW; j += 4) {
-                    const f32x4 x = *reinterpret_cast<const f32x4*>(vr + j);
-#pragma unroll
-                    for (int jj = 0; jj < 4; ++jj) vv[n][r][j + jj] = x[jj];
-                }
-            }
+            for (int m = 0; m < VW; ++m) vv[n][r][m] = vs[key * kRowF + VW * c + m];
         }
-
-    // all requests before the first product at D <= 64 (at D = 128 the rows
-    // held at once would cost occupancy)
+    // all operand reads issued before the first product at D <= 64 (at D = 128
+    // the operands held at once would cost occupancy)
     if constexpr (D <= 64) __builtin_amdgcn_sched_barrier(0);
-    // key tile by key tile, in the order the rows were requested: the products
-    // of a tile wait only for its own rows (every block of the grid loads at
-    // once, so the rows arrive over the whole HBM transfer)
+    // key tile by key tile, in the order the operands were read: the products
+    // of a tile wait only for its own reads
     f32x4 sacc[4];
 #pragma unroll
     for (int n = 0; n < 4; ++n) {
