@@ -3,6 +3,7 @@
 // here allocates device memory or synchronises: every call enqueues its
 // kernels on the caller's stream and returns.
 #include <stdarg.h>
+#include <algorithm>
 #include <stdio.h>
 #include <string.h>
 
@@ -179,14 +180,26 @@ struct ForwardBuffers {
     int64_t total;
 };
 
+// Chunks of the H_sum partials at head dims other than 128 (stats_cov_kernel:
+// one wave per (head, chunk, 32x32 tile of H)): about 2048 waves, at most 16
+// chunks per head.
+static void plan_cov(int bh, int blocks, int padded, int* chunks, int* chunk_blocks) {
+    const int per_chunk = bh * (padded / 32) * (padded / 32);
+    const int c = std::max(1, std::min((2048 + per_chunk - 1) / per_chunk, std::min(blocks, 16)));
+    *chunk_blocks = (blocks + c - 1) / c;
+    *chunks = (blocks + *chunk_blocks - 1) / *chunk_blocks;
+}
+
 // Means and routing buffers have the real head dim; the packed tables the
-// attention kernel reads have the padded one.  H_sum partials and the packed
-// H_sum^T exist only at head dim 128 (the only width with the first-order
-// term and HYD statistics).
+// attention kernel reads have the padded one.  The H_sum partials and the
+// packed H_sum^T have width 128 at head dim 128 (chunks of the statistics
+// kernel) and the padded width otherwise (chunks of plan_cov).
 static ForwardBuffers carve_forward(void* ws, int bh, int tokens, int head_dim, int exact, int esize) {
     const StatsPlan p = plan_stats(bh, tokens);
     const int padded = pisa::padded_head_dim(head_dim) ? pisa::padded_head_dim(head_dim) : head_dim;
-    const int cov_dim = head_dim == 128 ? head_dim : 0;
+    const int cov_dim = head_dim == 128 ? head_dim : padded;
+    int cov_chunks = p.chunks, cov_chunk_blocks = p.chunk_blocks;
+    if (head_dim != 128) plan_cov(bh, p.blocks, padded, &cov_chunks, &cov_chunk_blocks);
     const int64_t nd = (int64_t)bh * p.blocks * head_dim;
     const int64_t ndp = (int64_t)bh * p.blocks * padded;
     Carver c(ws);
@@ -196,7 +209,7 @@ static ForwardBuffers carve_forward(void* ws, int bh, int tokens, int head_dim, 
     f.kc = c.take<float>(nd * 4);
     f.vm = c.take<void>(nd * esize);
     f.hnorm = c.take<float>((int64_t)bh * p.blocks * 4);
-    f.hpart = c.take<float>((int64_t)bh * p.chunks * cov_dim * cov_dim * 4);
+    f.hpart = c.take<float>((int64_t)bh * cov_chunks * cov_dim * cov_dim * 4);
     f.kp = c.take<void>(ndp * pisa::kBlock * esize);
     f.vp = c.take<void>(ndp * pisa::kBlock * esize);
     f.kbar_pad = c.take<void>((int64_t)bh * p.npad * padded * esize);
@@ -264,14 +277,14 @@ static int validate_forward(int32_t dtype, int32_t batch, int32_t heads, int32_t
     if (batch <= 0 || heads <= 0 || tokens <= 0)
         return fail(PISA_ERR_INVALID_ARGUMENT, "PISA forward requires B>0, H>0, T>0");
     if (head_dim != 128) {
-        // generic_pisa.py:332-333: other head dims run without the first-order
-        // term, on centroid routing (no HYD bias, so no H_b norms)
+        // other head dims take the Triton statistics (generic_pisa.py:128-138,
+        // pisa_kernel.py:90-130: any head dim up to 256, H_sum included) and
+        // centroid routing (no HYD bias, so no H_b norms)
         if (!pisa::padded_head_dim(head_dim))
             return fail(PISA_ERR_UNSUPPORTED, "PISA forward supports head_dim a multiple of 8 up to 256, got %d",
                         head_dim);
-        if (stats_mode != PISA_STATS_GENERIC || route_mode != PISA_ROUTE_CENTROID || first_order)
-            return fail(PISA_ERR_UNSUPPORTED,
-                        "head_dim %d requires GENERIC statistics, CENTROID routing and no first-order term", head_dim);
+        if (stats_mode != PISA_STATS_GENERIC || route_mode != PISA_ROUTE_CENTROID)
+            return fail(PISA_ERR_UNSUPPORTED, "head_dim %d requires GENERIC statistics and CENTROID routing", head_dim);
     }
     const int bh = batch * heads;
     const StatsPlan p = plan_stats(bh, tokens);
@@ -349,6 +362,28 @@ static int prepare_impl(int32_t dtype, int32_t heads, int32_t tokens, int32_t he
         if ((rc = pisa::launch_kv_pack(dtype, padded, head_dim, sa.k, sa.v, sa.map, tokens, p.blocks, bh,
                                        static_cast<char*>(w.kp), static_cast<char*>(w.vp), st)))
             return rc;
+        if (first_order) {
+            // H_sum of the Triton statistics (pisa_kernel.py:80-84) from the
+            // block means just written, then dtype(H_sum)^T for the correction
+            pisa::CovArgs ca;
+            ca.k = sa.k;
+            ca.v = sa.v;
+            ca.map = sa.map;
+            ca.tokens = tokens;
+            ca.blocks = p.blocks;
+            ca.head_dim = head_dim;
+            plan_cov(bh, p.blocks, padded, &ca.chunks, &ca.chunk_blocks);
+            ca.kmean = w.kc;
+            ca.hpart = w.hpart;
+            if ((rc = pisa::launch_stats_cov(dtype, padded, ca, bh, st))) return rc;
+            pisa::ReduceArgs cr{};
+            cr.hpart = w.hpart;
+            cr.chunks = ca.chunks;
+            cr.ht = w.ht;
+            cr.blocks = p.blocks;
+            cr.npad = p.npad;
+            if ((rc = pisa::launch_cov_reduce(dtype, padded, cr, bh, st))) return rc;
+        }
         return route_impl(w, head_dim, exact_blocks, scale, sink_block, route_mode, debug_indices, debug_scores, p, bh,
                           st);
     }

@@ -325,10 +325,12 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
     const __amdgpu_buffer_rsrc_t vc_rs = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(TAIL ? a.vbar_t + (int64_t)bh * a.npad * D * sizeof(T) : a.vp), (short)0, cen_bytes, kRawFlags);
     const int lane_off = lane * 16;
-    // The first-order correction (head dim 128 only) needs the packed D x D
-    // matrix (32 fragments): the last iteration loads it into kf (fragments
-    // 0..15) and vf (16..31) in place of the next chunk.
-    const bool first_order = TAIL && D == 128 && a.ht != nullptr;
+    // The first-order correction needs the packed D x D matrix (fragment md*KT
+    // + t: rows 32md.., columns 16t..): the last iteration loads its first two
+    // 32-row tiles into kf and, up to D = 128, the rest into vf, in place of the
+    // next chunk; above 128 (more fragments than kf and vf hold) the epilogue
+    // loads the tiles from the third on, one ahead of their products.
+    const bool first_order = TAIL && a.ht != nullptr;
     const __amdgpu_buffer_rsrc_t ht_rs = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(first_order ? a.ht + (int64_t)bh * D * D * sizeof(T) : a.kp), (short)0,
         first_order ? D * D * (int)sizeof(T) : 0, kRawFlags);
@@ -556,7 +558,7 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
             const Src kn = (first_order && last) ? Src{ht_rs, 0}
                            : exact_k ? Src{kp_rs, row1 * (int)kBlockBytes}
                            : tail_k  ? Src{kc_rs, row1 * (int)kBlockBytes} : kptr(cc + 1, row1);
-            const Src vn = (first_order && last) ? Src{ht_rs, 16 * 1024}
+            const Src vn = (first_order && last) ? Src{ht_rs, 2 * KT * 1024}
                            : exact_k ? Src{vp_rs, row1 * (int)kBlockBytes}
                            : tail_k  ? Src{vc_rs, row1 * (int)kBlockBytes} : vptr(cc + 1, row1);
             const Src kn2 = (first_order && last) ? Src{ht_rs, 0}
@@ -647,16 +649,20 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
         for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
             for (int v = 0; v < 16; ++v) corr[nt][v] = 0.0f;
-        if constexpr (D == 128) {
-            if (first_order) {
-                // packed D x D matrix fragment (md, t): rows 32md.., columns 16t..
-                // (kfrag_elem), in kf (md < 2) and vf (md >= 2) since the last iteration
+        if (first_order) {
+            // packed D x D matrix fragment (md, t): rows 32md.., columns 16t..
+            // (kfrag_elem), in kf (md < 2) and up to D = 128 in vf (md >= 2)
+            // since the last iteration; above 128 tile md + 1 is loaded into
+            // kf[(md + 1) % 2] here (tile md - 1 used it last)
+            if constexpr (D > 128)
+                if (md + 1 < MD && md + 1 >= 2) load_k_half(kf[(md + 1) & 1], Src{ht_rs, 0}, md + 1);
+            uint32_t qoff = lane * 16;
+            if constexpr (QLDS) asm volatile("" : "+v"(qoff));
 #pragma unroll
-                for (int t = 0; t < KT; ++t) {
-                    const vec8 hf = md < 2 ? kf[md & 1][t] : vf[(md >= 2 ? md - 2 : 0) * 2 + t / 4][t % 4];
+            for (int t = 0; t < KT; ++t) {
+                const vec8 hf = (D > 128 || md < 2) ? kf[md & 1][t] : vf[(md >= 2 ? md - 2 : 0) * 2 + t / 4][t % 4];
 #pragma unroll
-                    for (int nt = 0; nt < NT; ++nt) corr[nt] = mfma32(hf, qreg[nt][t], corr[nt]);
-                }
+                for (int nt = 0; nt < NT; ++nt) corr[nt] = mfma32(hf, qfrag(nt, t, qoff), corr[nt]);
             }
         }
 #pragma unroll

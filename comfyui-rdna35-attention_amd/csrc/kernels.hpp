@@ -44,17 +44,16 @@ struct ReduceArgs {
     int blocks, npad;
 };
 
-// One 32x32 tile (tile = 4 * row tile + column tile) of the H_sum reduction of
-// head bh, by 256 threads: the per-chunk partials are added in chunk order
-// (the sum does not depend on how the loads are batched), H_sum is written in
-// fp32 and its transpose as packed dtype fragments (both optional).
-// `tile_lds` is a 32 x 33 float array; the call ends with a barrier, so it can
-// be called again on the same array.
-template <typename T>
+// One 32x32 tile (tile = (D/32) * row tile + column tile) of the H_sum
+// reduction of head bh at width D, by 256 threads: the per-chunk partials are
+// added in chunk order (the sum does not depend on how the loads are
+// batched), H_sum is written in fp32 and its transpose as packed dtype
+// fragments (both optional).  `tile_lds` is a 32 x 33 float array; the call
+// ends with a barrier, so it can be called again on the same array.
+template <typename T, int D = 128>
 __device__ inline void reduce_h_tile(const ReduceArgs& a, int bh, int tile, float (*tile_lds)[33], int t) {
-    constexpr int D = 128;
-    const int tr = tile >> 2;  // 32-row tile index
-    const int tc = tile & 3;   // 32-col tile index
+    const int tr = tile / (D / 32);  // 32-row tile index
+    const int tc = tile % (D / 32);  // 32-col tile index
     const float* src = a.hpart + (int64_t)bh * a.chunks * D * D;
     float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     int64_t off[4];
@@ -162,6 +161,22 @@ struct LayoutArgs {
 };
 
 int launch_stats(int dtype, int mode, const StatsArgs& a, int bh_count, hipStream_t stream);
+// H_sum partials of the generic statistics at a padded head dim other than 128
+// (the statistics kernel forms them at 128): H_b = dtype(K_b - k_bar_b)^T V_b
+// summed over each chunk of chunk_blocks blocks, one wave per (head, chunk,
+// 32x32 tile of H).  kmean holds the fp32 block means of K that the means
+// kernel wrote ([BH][N][head_dim]).
+struct CovArgs {
+    View k, v;
+    TokenMap map;
+    int tokens, blocks, head_dim, chunk_blocks, chunks;
+    const float* kmean;
+    float* hpart;  // [BH][chunks][Dp][Dp]
+};
+int launch_stats_cov(int dtype, int padded, const CovArgs& a, int bh_count, hipStream_t stream);
+// Chunk-order sum of launch_stats_cov's partials into dtype(H_sum)^T packed at
+// the padded width (ReduceArgs.ht; hsum optional).
+int launch_cov_reduce(int dtype, int padded, const ReduceArgs& a, int bh_count, hipStream_t stream);
 int launch_stats_reduce(int dtype, const ReduceArgs& a, int bh_count, hipStream_t stream);
 int launch_route(const RouteArgs& a, hipStream_t stream);
 // Routing with the H_sum reduction of head dim 128 (stats_reduce_kernel's work,

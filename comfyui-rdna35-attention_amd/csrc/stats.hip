@@ -320,9 +320,9 @@ __global__ __launch_bounds__(256) void stats_reduce_kernel(ReduceArgs a) {
     if (blockIdx.x == 0) zero_centroid_pad<T>(a, blockIdx.y, threadIdx.x);
 }
 
-// Block means of the generic path at head dims other than 128 (the
-// reference uses the first-order term only at 128, generic_pisa.py:332, so
-// no H_sum is formed): one 256-thread workgroup per (batch*head, block).
+// Block means of the generic path at head dims other than 128 (H_sum, when
+// the first-order term is asked for, comes from stats_cov_kernel below): one
+// 256-thread workgroup per (batch*head, block).
 // Thread (row group rr, piece pc) sums the 8 dims pc*8.. of rows rr, rr+R, ..
 // in fp32; an LDS pass adds the R row groups in order, and means are
 // sum / len (generic_pisa.py:128-132, pisa_kernel.py:72-77).  Writes the
@@ -432,6 +432,126 @@ int launch_stats_means_t(int padded, const StatsArgs& a, int bh_count, hipStream
 int launch_stats_means(int dtype, int padded, const StatsArgs& a, int bh_count, hipStream_t stream) {
     if (dtype == PISA_DTYPE_BF16) return launch_stats_means_t<bf16_t>(padded, a, bh_count, stream);
     return launch_stats_means_t<f16_t>(padded, a, bh_count, stream);
+}
+
+// H_sum partials of the generic statistics for head dims other than 128
+// (pisa_kernel.py:71-84, the Triton statistics every head dim up to 256 takes:
+// centred keys rounded to the input dtype, H_b = centred^T V accumulated in
+// fp32).  One wave per (head, chunk of blocks, 32x32 tile (tr, tc) of H): for
+// each block it reads the block's 32 key dims of row slice tr and 32 value dims
+// of column slice tc (16-byte pieces, token order from the grid map), centres
+// the keys on the fp32 means of the means kernel, stages both slices transposed
+// in LDS (dim-major, 4 consecutive tokens per 8-byte write) and accumulates
+// H[32tr + i][32tc + j] with four 32x32x16 MFMAs (tokens as the contraction).
+// Rows past a short last block contribute zero, as their zero values make
+// them contribute in the reference.  The partial of each chunk is written once
+// (no float atomics; the reference adds with tl.atomic_add).
+template <typename T, int DP>
+__global__ __launch_bounds__(64) void stats_cov_kernel(CovArgs a) {
+    typedef typename Elem<T>::vec8 vec8;
+    typedef T vec4 __attribute__((ext_vector_type(4)));
+    constexpr int TD = DP / 32;
+    constexpr int kRowT = kBlock + 8;  // padded LDS row (tokens) of a transposed slice
+    __shared__ __attribute__((aligned(16))) T kts[32 * kRowT];
+    __shared__ __attribute__((aligned(16))) T vts[32 * kRowT];
+    const int lane = threadIdx.x;
+    const int tile = blockIdx.x % (TD * TD);
+    const int rest = blockIdx.x / (TD * TD);
+    const int chunk = rest % a.chunks;
+    const int bh = rest / a.chunks;
+    const int tr = tile / TD;
+    const int tc = tile % TD;
+    const int first = chunk * a.chunk_blocks;
+    const int last = min(a.blocks, first + a.chunk_blocks);
+    const int pc = lane & 3;    // 8-dim piece of the slices
+    const int q4 = lane >> 2;   // tokens 4 q4 .. 4 q4 + 3
+    const int dk = 32 * tr + 8 * pc;
+    const int dv = 32 * tc + 8 * pc;
+    const bool kdims = dk < a.head_dim;  // head_dim is a multiple of 8
+    const bool vdims = dv < a.head_dim;
+    const int col = lane & 31;
+    const int half = lane >> 5;
+    f32x16 acc;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
+    for (int b = first; b < last; ++b) {
+        const int len = min(kBlock, a.tokens - b * kBlock);
+        const int base = a.map.block_base(b);
+        float mean[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            mean[e] = kdims ? a.kmean[((int64_t)bh * a.blocks + b) * a.head_dim + dk + e] : 0.0f;
+        vec8 kx[4], vx[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int raster = base + a.map.intra_offset(min(4 * q4 + r, len - 1));
+            if (kdims) kx[r] = load8<vec8>(a.k.data + (a.k.row(bh, raster) + dk) * (int64_t)sizeof(T));
+            if (vdims) vx[r] = load8<vec8>(a.v.data + (a.v.row(bh, raster) + dv) * (int64_t)sizeof(T));
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            vec4 ck, cv;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const bool valid = 4 * q4 + r < len;
+                ck[r] = (valid && kdims) ? from_f32<T>(to_f32(kx[r][e]) - mean[e]) : T(0.0f);
+                cv[r] = (valid && vdims) ? vx[r][e] : T(0.0f);
+            }
+            *reinterpret_cast<vec4*>(&kts[(8 * pc + e) * kRowT + 4 * q4]) = ck;
+            *reinterpret_cast<vec4*>(&vts[(8 * pc + e) * kRowT + 4 * q4]) = cv;
+        }
+        // one wave: its LDS writes and reads stay in program order
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            const vec8 ka = *reinterpret_cast<const vec8*>(&kts[col * kRowT + 16 * st + 8 * half]);
+            const vec8 vb = *reinterpret_cast<const vec8*>(&vts[col * kRowT + 16 * st + 8 * half]);
+            acc = mfma32(ka, vb, acc);
+        }
+    }
+    float* dst = a.hpart + ((int64_t)bh * a.chunks + chunk) * DP * DP;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+        const int row = 32 * tr + 8 * (v >> 2) + 4 * half + (v & 3);
+        dst[row * DP + 32 * tc + col] = acc[v];
+    }
+}
+
+template <typename T, int DP>
+__global__ __launch_bounds__(256) void cov_reduce_kernel(ReduceArgs a) {
+    __shared__ float tile[32][33];
+    reduce_h_tile<T, DP>(a, blockIdx.y, blockIdx.x, tile, threadIdx.x);
+}
+
+template <typename T, int DP>
+static void launch_cov_dp(const CovArgs& a, const ReduceArgs* r, int bh_count, hipStream_t stream) {
+    constexpr int tiles = (DP / 32) * (DP / 32);
+    if (r) hipLaunchKernelGGL((cov_reduce_kernel<T, DP>), dim3(tiles, bh_count), dim3(256), 0, stream, *r);
+    else hipLaunchKernelGGL((stats_cov_kernel<T, DP>), dim3(bh_count * a.chunks * tiles), dim3(64), 0, stream, a);
+}
+
+template <typename T>
+static int launch_cov_t(int padded, const CovArgs& a, const ReduceArgs* r, int bh_count, hipStream_t stream) {
+    switch (padded) {
+        case 64: launch_cov_dp<T, 64>(a, r, bh_count, stream); break;
+        case 96: launch_cov_dp<T, 96>(a, r, bh_count, stream); break;
+        case 128: launch_cov_dp<T, 128>(a, r, bh_count, stream); break;  // head dims 104..120
+        case 160: launch_cov_dp<T, 160>(a, r, bh_count, stream); break;
+        case 192: launch_cov_dp<T, 192>(a, r, bh_count, stream); break;
+        case 256: launch_cov_dp<T, 256>(a, r, bh_count, stream); break;
+        default: return pisa_host::fail(PISA_ERR_UNSUPPORTED, "H_sum: padded head dim %d", padded);
+    }
+    return pisa_host::check_launch(r ? "cov_reduce_kernel" : "stats_cov_kernel");
+}
+
+int launch_stats_cov(int dtype, int padded, const CovArgs& a, int bh_count, hipStream_t stream) {
+    if (dtype == PISA_DTYPE_BF16) return launch_cov_t<bf16_t>(padded, a, nullptr, bh_count, stream);
+    return launch_cov_t<f16_t>(padded, a, nullptr, bh_count, stream);
+}
+
+int launch_cov_reduce(int dtype, int padded, const ReduceArgs& r, int bh_count, hipStream_t stream) {
+    const CovArgs none{};
+    if (dtype == PISA_DTYPE_BF16) return launch_cov_t<bf16_t>(padded, none, &r, bh_count, stream);
+    return launch_cov_t<f16_t>(padded, none, &r, bh_count, stream);
 }
 
 template <typename T, int MODE>

@@ -33,7 +33,7 @@ __version__ = "1.0.0"
 
 BLOCK_SIZE = 64
 HEAD_DIM = 128
-GENERIC_HEAD_DIMS = tuple(range(8, 257, 8))  # generic PISA (no first-order term off 128) and dense attention
+GENERIC_HEAD_DIMS = tuple(range(8, 257, 8))  # generic PISA (first-order term included) and dense attention
 MAX_BLOCKS = 1024
 MAX_TOKENS = BLOCK_SIZE * MAX_BLOCKS
 SPATIAL_SIDE = 96

@@ -29,8 +29,9 @@ BLOCK_SIZE = 64
 MIN_TOKENS = 8192
 SPATIAL_BLOCK_EDGE = 8
 # Head dims the HIP kernels take (multiples of 8 up to 256; dims are padded to
-# 64/96/128/160/192/256 inside).  The first-order term runs at 128 bf16 only,
-# as in the reference (generic_pisa.py:332).
+# 64/96/128/160/192/256 inside).  The ComfyUI override asks for the
+# first-order term at 128 bf16 only, as the reference's does
+# (generic_pisa.py:332); a direct call gets it at any of these widths.
 SUPPORTED_HEAD_DIMS = tuple(range(8, 257, 8))
 
 
@@ -143,8 +144,8 @@ def generic_pisa_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
     grid_sizes=(frames, height, width) declares a raster token grid; blocks are
     then its per-frame 8x8 tiles (the layout the reference obtains by packing).
     Statistics follow the reference's choice for the shape (_block_stats); the
-    first-order term exists at head dim 128 (the only width whose statistics
-    kernel forms H_sum), so other widths need use_first_order=False.
+    first-order term is applied at every head dim, as the reference's Triton
+    statistics form H_sum at any width up to 256 (pisa_kernel.py:90-130).
     """
     if q.ndim != 3 or q.shape != k.shape or q.shape != v.shape:
         raise ValueError("generic PISA requires matching [BH,T,D] q/k/v")
@@ -156,9 +157,6 @@ def generic_pisa_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
         raise ValueError("generic PISA requires q/k/v on one CUDA/HIP device")
     if q.shape[-1] not in SUPPORTED_HEAD_DIMS:
         raise ValueError(f"generic PISA HIP kernels support head_dim {SUPPORTED_HEAD_DIMS}, got {q.shape[-1]}")
-    if use_first_order and q.shape[-1] != 128:
-        raise ValueError(f"generic PISA computes the first-order term at head_dim 128 only (got {q.shape[-1]}); "
-                         f"pass use_first_order=False")
     bh, tokens, head_dim = q.shape
     blocks = math.ceil(tokens / BLOCK_SIZE)
     exact_blocks = min(blocks, max(1, math.ceil(exact_budget * blocks)))

@@ -152,9 +152,9 @@ PISA_HIP_EXPORT int64_t pisa_hip_forward_workspace_bytes(int32_t batch, int32_t 
  * spatial variant (_forward_spatial_bhtd_op, __init__.py:344-365, with the
  * fused epilogue of pisa_kernels.cu:296-340) and generic_pisa_attention
  * (generic_pisa.py:141-232).
- *   head_dim       128, or any multiple of 8 up to 256 with PISA_STATS_GENERIC,
- *                  PISA_ROUTE_CENTROID and first_order 0 (generic_pisa.py:332-333
- *                  uses the first-order term only at 128 bf16)
+ *   head_dim       128, or any multiple of 8 up to 256 with PISA_STATS_GENERIC and
+ *                  PISA_ROUTE_CENTROID (first_order at any of them: the Triton
+ *                  statistics of generic_pisa.py:128-138 form H_sum at every width)
  *   stats_mode     PISA_STATS_HYD or PISA_STATS_GENERIC
  *   route_mode     PISA_ROUTE_HYD or PISA_ROUTE_CENTROID
  *   first_order    1 adds C = s/T * q . bf16(H_sum) weighted by the tail mass

@@ -90,13 +90,13 @@ def test_forward_validation_rejects_before_any_launch(lib):
                                         over.get("grid", grid), a["exact"], a["scale"], a["sink"], a["stats"],
                                         a["route"], a["first"], None, None, None, 0, None)
 
-    assert call(head_dim=64) == 2                      # HYD statistics / first order only at 128
+    assert call(head_dim=64) == 2                      # HYD statistics only at 128
     generic = dict(stats=lib.STATS_GENERIC, route=lib.ROUTE_CENTROID, first=0)
     assert call(head_dim=100, **generic) == 2          # not a multiple of 8
     assert call(head_dim=264, **generic) == 2          # above 256
-    assert call(head_dim=64, **{**generic, "first": 1}) == 2   # no first-order term off 128
     assert call(head_dim=64, **{**generic, "route": lib.ROUTE_HYD}) == 2
     assert call(head_dim=64, **generic) == 3           # supported: fails only for the missing workspace
+    assert call(head_dim=64, **{**generic, "first": 1}) == 3   # first-order term at any width, as the reference's
     assert call(dtype=2) == 2                          # fp32 not supported by PISA
     assert call(exact=144) == 1                        # dense goes to attn_hip_dense_forward
     assert call(exact=0, sink=0) == 1                  # sink needs an exact block
