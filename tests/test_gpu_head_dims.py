@@ -54,15 +54,19 @@ def test_generic_forward_head_dims_match_oracle(native, head_dim, dtype, tokens,
     assert_close(np32(out), expected, TOL[dtype], TOL[dtype], f"generic D={head_dim}")
 
 
-@pytest.mark.parametrize("head_dim,grid", [(80, (2, 16, 32)), (64, (1, 32, 32)), (160, (1, 24, 32))])
-def test_generic_forward_head_dims_on_token_grids(native, head_dim, grid):
+@pytest.mark.parametrize("head_dim,grid,first_order", [(80, (2, 16, 32), False), (64, (1, 32, 32), False),
+                                                       (160, (1, 24, 32), False), (80, (2, 16, 32), True),
+                                                       (192, (1, 16, 32), True)])
+def test_generic_forward_head_dims_on_token_grids(native, head_dim, grid, first_order):
     tokens = math.prod(grid)
     gen = torch.Generator().manual_seed(head_dim + tokens)
     q4, k4, v4 = (torch.randn((1, 2, tokens, head_dim), generator=gen).to(torch.float16).cuda() for _ in range(3))
+    if first_order:  # values correlated with keys: a first-order term well above the tolerance
+        v4 = 2 * k4 + 0.1 * v4
     exact = 3
-    out = native.generic_forward(q4, k4, v4, exact, 1 / math.sqrt(head_dim), False, token_grid=grid)
+    out = native.generic_forward(q4, k4, v4, exact, 1 / math.sqrt(head_dim), first_order, token_grid=grid)
     packed = [spatial_to_packed(t, *grid) for t in (q4, k4, v4)]
-    ref = opisa.generic_forward(*packed, exact, first_order=False, dtype="f16")
+    ref = opisa.generic_forward(*packed, exact, first_order=first_order, dtype="f16")
     expected = packed_to_merged(ref, 1, 2, *grid)
     assert_close(np32(out).reshape(1, tokens, 2 * head_dim), expected, 2e-2, 2e-2, f"grid D={head_dim}")
 
