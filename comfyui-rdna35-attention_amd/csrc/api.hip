@@ -389,7 +389,7 @@ static int prepare_impl(int32_t dtype, int32_t heads, int32_t tokens, int32_t he
     }
     if ((rc = pisa::launch_stats(dtype, stats_mode, sa, bh, st))) return rc;
 
-    pisa::ReduceArgs ra;
+    pisa::ReduceArgs ra{};
     ra.hpart = w.hpart;
     ra.chunks = p.chunks;
     ra.hsum = nullptr;
@@ -577,7 +577,12 @@ int pisa_hip_forward_noalloc(int32_t dtype, int32_t batch, int32_t heads, int32_
 int64_t pisa_hip_block_stats_workspace_bytes(int32_t batch, int32_t heads, int32_t tokens, int32_t head_dim) {
     if (batch <= 0 || heads <= 0 || tokens <= 0 || head_dim <= 0) return 0;
     const StatsPlan p = plan_stats(batch * heads, tokens);
-    return (int64_t)batch * heads * p.chunks * head_dim * head_dim * 4;
+    if (head_dim == 128) return (int64_t)batch * heads * p.chunks * head_dim * head_dim * 4;
+    const int padded = pisa::padded_head_dim(head_dim);
+    if (!padded) return 0;
+    int chunks, chunk_blocks;
+    plan_cov(batch * heads, p.blocks, padded, &chunks, &chunk_blocks);
+    return (int64_t)batch * heads * chunks * padded * padded * 4;
 }
 
 int pisa_hip_block_stats(int32_t dtype, int32_t out_dtype, int32_t batch, int32_t heads, int32_t tokens,
@@ -588,12 +593,23 @@ int pisa_hip_block_stats(int32_t dtype, int32_t out_dtype, int32_t batch, int32_
     if (out_dtype != dtype && out_dtype != PISA_DTYPE_F32)
         return fail(PISA_ERR_INVALID_ARGUMENT, "out_dtype must equal dtype or be float32");
     if (batch <= 0 || heads <= 0 || tokens <= 0) return fail(PISA_ERR_INVALID_ARGUMENT, "requires B>0, H>0, T>0");
-    if (head_dim != 128) return fail(PISA_ERR_UNSUPPORTED, "block statistics require head_dim=128, got %d", head_dim);
     if (stats_mode != PISA_STATS_MEANS && stats_mode != PISA_STATS_HYD && stats_mode != PISA_STATS_GENERIC)
         return fail(PISA_ERR_INVALID_ARGUMENT, "unknown stats_mode %d", stats_mode);
+    // head dims other than 128: the Triton statistics of pisa_kernel.py:90-130
+    // (any width up to 256, no H_b norms), here at multiples of 8
+    const int padded = head_dim == 128 ? 128 : pisa::padded_head_dim(head_dim);
+    if (head_dim != 128) {
+        if (!padded)
+            return fail(PISA_ERR_UNSUPPORTED, "block statistics support head_dim a multiple of 8 up to 256, got %d",
+                        head_dim);
+        if (stats_mode == PISA_STATS_HYD)
+            return fail(PISA_ERR_UNSUPPORTED, "HYD statistics require head_dim=128, got %d", head_dim);
+        if (h_norm) return fail(PISA_ERR_INVALID_ARGUMENT, "h_norm is formed at head_dim=128 only (pass null)");
+    }
     if (!q_centroids || !k_centroids || !v_means) return fail(PISA_ERR_INVALID_ARGUMENT, "centroid outputs are required");
     const bool cov = stats_mode != PISA_STATS_MEANS;
-    if (cov && (!h_sum || !h_norm)) return fail(PISA_ERR_INVALID_ARGUMENT, "h_sum and h_norm are required");
+    if (cov && (!h_sum || (head_dim == 128 && !h_norm)))
+        return fail(PISA_ERR_INVALID_ARGUMENT, head_dim == 128 ? "h_sum and h_norm are required" : "h_sum is required");
     int rc;
     if ((rc = check_grid(grid, tokens)) || (rc = check_view("q", q, 2, true)) || (rc = check_view("k", k, 2, true)) ||
         (rc = check_view("v", v, 2, true)))
@@ -625,6 +641,29 @@ int pisa_hip_block_stats(int32_t dtype, int32_t out_dtype, int32_t batch, int32_
     sa.hpart = cov ? static_cast<float*>(workspace) : nullptr;
     sa.npad = p.npad;
     sa.head_dim = head_dim;
+    if (head_dim != 128) {
+        if ((rc = pisa::launch_stats_means(dtype, padded, sa, bh, st))) return rc;
+        if (!cov) return PISA_OK;
+        pisa::CovArgs ca;
+        ca.k = sa.k;
+        ca.v = sa.v;
+        ca.map = sa.map;
+        ca.tokens = tokens;
+        ca.blocks = p.blocks;
+        ca.head_dim = head_dim;
+        plan_cov(bh, p.blocks, padded, &ca.chunks, &ca.chunk_blocks);
+        ca.kmean = k_centroids;
+        ca.hpart = static_cast<float*>(workspace);
+        if ((rc = pisa::launch_stats_cov(dtype, padded, ca, bh, st))) return rc;
+        pisa::ReduceArgs cr{};
+        cr.hpart = ca.hpart;
+        cr.chunks = ca.chunks;
+        cr.hsum = h_sum;
+        cr.hsum_dim = head_dim;
+        cr.blocks = p.blocks;
+        cr.npad = p.npad;
+        return pisa::launch_cov_reduce(dtype, padded, cr, bh, st);
+    }
     if ((rc = pisa::launch_stats(dtype, stats_mode, sa, bh, st))) return rc;
     if (!cov) return PISA_OK;
     pisa::ReduceArgs ra;

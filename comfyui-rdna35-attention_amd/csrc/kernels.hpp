@@ -37,7 +37,8 @@ struct StatsArgs {
 struct ReduceArgs {
     const float* hpart;
     int chunks;
-    float* hsum;       // [BH][D][D] (nullable)
+    float* hsum;       // [BH][hsum_dim][hsum_dim] (nullable): the first hsum_dim rows and columns
+    int hsum_dim;      // 0: the reduction's width
     void* ht;          // [BH] packed D x D, element (c, r) = dtype(H_sum[r][c]) (nullable)
     void* kbar_pad;    // nullable
     void* vbar_t_pad;  // nullable
@@ -73,9 +74,12 @@ __device__ inline void reduce_h_tile(const ReduceArgs& a, int bh, int tile, floa
             for (int it = 0; it < 4; ++it)
                 if (ch0 + u < a.chunks) s[it] += x[u][it];
     }
+    const int hd = a.hsum_dim > 0 ? a.hsum_dim : D;
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
-        if (a.hsum) a.hsum[(int64_t)bh * D * D + off[it]] = s[it];
+        const int r = tr * 32 + it * 8 + (t >> 5);
+        const int c = tc * 32 + (t & 31);
+        if (a.hsum && r < hd && c < hd) a.hsum[((int64_t)bh * hd + r) * hd + c] = s[it];
         tile_lds[it * 8 + (t >> 5)][t & 31] = s[it];
     }
     __syncthreads();

@@ -397,6 +397,7 @@ __global__ __launch_bounds__(256) void stats_means_kernel(StatsArgs a) {
         else static_cast<T*>(a.vm_out)[o] = from_f32<T>(mv);
         if (a.qc_route) a.qc_route[o] = mq;
     }
+    if (!a.kbar_pad) return;  // the standalone statistics entry point wants no packed centroids
     const int64_t head_base = (int64_t)bh * a.npad * DP;
     T* kbar = static_cast<T*>(a.kbar_pad);
     T* vbar = static_cast<T*>(a.vbar_t_pad);

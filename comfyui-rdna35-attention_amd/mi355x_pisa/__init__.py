@@ -378,7 +378,8 @@ def _fixed_block_op_fake(q, k, v, scale, causal, mask):
 
 # --------------------------------------------------------------------------- statistics
 def _block_stats(q, k, v, mode, out_dtype):
-    """q/k/v: [BH,T,D] (or [B,H,T,D] views).  Returns the 5 HYD outputs (3 for MEANS)."""
+    """q/k/v: [BH,T,D] (or [B,H,T,D] views).  Returns the 5 HYD outputs (3 for MEANS); at head dims other than
+    128 (GENERIC or MEANS statistics) h_norm is None."""
     q4 = q if q.ndim == 4 else _as4(q)
     k4 = k if k.ndim == 4 else _as4(k)
     v4 = v if v.ndim == 4 else _as4(v)
@@ -391,7 +392,7 @@ def _block_stats(q, k, v, mode, out_dtype):
     v_means = q.new_empty(shape, dtype=out_dtype)
     cov = mode != _lib.STATS_MEANS
     h_sum = q.new_empty((bh, head_dim, head_dim), dtype=torch.float32) if cov else None
-    h_norm = q.new_empty((bh, blocks), dtype=torch.float32) if cov else None
+    h_norm = q.new_empty((bh, blocks), dtype=torch.float32) if cov and head_dim == HEAD_DIM else None  # 128 only
     with on_device(q.device):
         ws_bytes = LIB.pisa_hip_block_stats_workspace_bytes(batch, heads, tokens, head_dim) if cov else 0
         workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)

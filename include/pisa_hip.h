@@ -229,7 +229,10 @@ PISA_HIP_EXPORT int64_t pisa_hip_block_stats_workspace_bytes(int32_t batch, int3
  *   k_centroids  [BH,N,D] float32
  *   v_means      [BH,N,D] in out_dtype
  *   h_sum        [BH,D,D] float32, nullable for PISA_STATS_MEANS
- *   h_norm       [BH,N]   float32, nullable for PISA_STATS_MEANS
+ *   h_norm       [BH,N]   float32, nullable for PISA_STATS_MEANS; null at head dims
+ *                other than 128
+ *   head_dim     128, or (PISA_STATS_GENERIC / PISA_STATS_MEANS) a multiple of 8 up
+ *                to 256, as pisa_prepare_triton takes any width up to 256
  * H_sum is reduced deterministically (no floating-point atomics).
  */
 PISA_HIP_EXPORT int pisa_hip_block_stats(int32_t dtype, int32_t out_dtype, int32_t batch, int32_t heads,

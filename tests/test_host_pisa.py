@@ -584,3 +584,18 @@ def test_h3_override_chains_unsupported_calls_and_patch_rules():
         kept, info = h3.patch_minimax_h3_attention(model, enabled=True, verbose_fallbacks=False)
     assert kept is model and "container-aware" in info
     assert h3.patch_minimax_h3_attention(H3Model(), enabled=True, verbose_fallbacks=False)[0] is not None
+
+
+def test_pisa_prepare_validation_matches_the_reference_messages():
+    """pisa_prepare_triton's checks in the reference's order and words (pisa_kernel.py:96-111)."""
+    from rdna35_block_attention.pisa_kernel import pisa_prepare_triton
+
+    k = torch.zeros((2, 64, 64), dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match=r"matching \[BH,T,D\] k/v"):
+        pisa_prepare_triton(k[0], k[0])
+    with pytest.raises(ValueError, match="block_size=64"):
+        pisa_prepare_triton(k, k, block_size=32)
+    with pytest.raises(ValueError, match="fp16/bf16"):
+        pisa_prepare_triton(k.float(), k.float())
+    with pytest.raises(ValueError, match="CUDA/HIP tensors"):
+        pisa_prepare_triton(k, k)
