@@ -599,3 +599,20 @@ def test_pisa_prepare_validation_matches_the_reference_messages():
         pisa_prepare_triton(k.float(), k.float())
     with pytest.raises(ValueError, match="CUDA/HIP tensors"):
         pisa_prepare_triton(k, k)
+
+
+def test_fixed_block_triton_name_validation_matches_the_reference_messages():
+    """fixed_block_attention_triton_bh's checks in the reference's order and words (triton_kernel.py:209-223)."""
+    from rdna35_block_attention.triton_kernel import fixed_block_attention_triton_bh
+
+    q = torch.zeros((2, 64, 64), dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="expects \\[BH,T,D\\], got rank 2"):
+        fixed_block_attention_triton_bh(q[0], q[0], q[0])
+    with pytest.raises(ValueError, match="identical q/k/v shapes"):
+        fixed_block_attention_triton_bh(q, q[:, :32], q)
+    with pytest.raises(ValueError, match="block_size=64"):
+        fixed_block_attention_triton_bh(q, q, q, block_size=32)
+    with pytest.raises(ValueError, match="fp16/bf16 only"):
+        fixed_block_attention_triton_bh(q.float(), q.float(), q.float())
+    with pytest.raises(ValueError, match="CUDA/HIP device tensor"):
+        fixed_block_attention_triton_bh(q, q, q)
