@@ -6,7 +6,8 @@ full_attention_*, pisa_attention, the layout/reference helpers and the
 ComfyUI override factories in the submodules - backed by the gfx950 HIP
 kernels of ``mi355x_pisa``.
 """
-from .diagnostics import detect_runtime, explain_dispatch, get_device_name, is_rocm_pytorch, native_status
+from .diagnostics import (detect_runtime, explain_dispatch, get_device_name, has_triton, is_rocm_pytorch,
+                          native_status)
 from .dispatch import fixed_block_attention
 from .full_attention import full_attention_hip, full_attention_triton
 from .pisa_attention import pisa_attention
@@ -21,6 +22,7 @@ __all__ = [
     "full_attention_hip",
     "full_attention_triton",
     "get_device_name",
+    "has_triton",
     "is_rocm_pytorch",
     "native_status",
     "pisa_attention",

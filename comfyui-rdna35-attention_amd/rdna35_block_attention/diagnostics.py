@@ -70,6 +70,28 @@ def load_native():
     return mi355x_pisa
 
 
+def has_triton(import_module: bool = True) -> tuple[bool, str]:
+    """(available, version or reason) of a Triton install - the reference's probe of the same name
+    (diagnostics.py:79); nothing in this package runs Triton, the report is for callers that ask."""
+    import importlib.metadata
+    import importlib.util
+
+    if importlib.util.find_spec("triton") is None:
+        return False, "triton module not found"
+    if not import_module:
+        for dist in ("triton", "triton-windows"):
+            try:
+                return True, importlib.metadata.version(dist)
+            except importlib.metadata.PackageNotFoundError:
+                continue
+        return True, "installed"
+    try:
+        import triton
+    except Exception as exc:
+        return False, f"{type(exc).__name__}: {exc}"
+    return True, str(getattr(triton, "__version__", "installed"))
+
+
 def native_status() -> tuple[bool, str]:
     """(loaded, implementation or the load error) of the gfx950 HIP library."""
     try:

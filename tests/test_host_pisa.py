@@ -616,3 +616,17 @@ def test_fixed_block_triton_name_validation_matches_the_reference_messages():
         fixed_block_attention_triton_bh(q.float(), q.float(), q.float())
     with pytest.raises(ValueError, match="CUDA/HIP device tensor"):
         fixed_block_attention_triton_bh(q, q, q)
+
+
+def test_reference_module_and_probe_names_resolve():
+    """Callers importing the reference's module names get this package's objects."""
+    import rdna35_block_attention as rba
+    from rdna35_block_attention import minimax_h3_attention as h3
+    from rdna35_block_attention import minimax_h3_gfx1151_attention as h3_ref_name
+
+    assert h3_ref_name.make_minimax_h3_gfx1151_attention_override is h3.make_minimax_h3_attention_override
+    assert h3_ref_name.patch_minimax_h3_gfx1151_attention is h3.patch_minimax_h3_attention
+    assert h3_ref_name.pack_minimax_h3_qkv is h3.pack_minimax_h3_qkv
+    available, detail = rba.has_triton(import_module=False)
+    assert isinstance(available, bool) and isinstance(detail, str)
+    assert "has_triton" in rba.__all__
