@@ -10,6 +10,11 @@ from __future__ import annotations
 
 from .minimax_h3_attention import (  # noqa: F401
     LOG_PREFIX,
+    MINIMAX_H3_HEAD_DIM,
+    MINIMAX_H3_HEADS,
+    MINIMAX_H3_MAX_PACK_TOKENS,
+    MINIMAX_H3_MIN_PACK_TOKENS,
+    MINIMAX_H3_PACK_ALL_TOKENS,
     make_minimax_h3_attention_override,
     minimax_h3_pack_profile,
     pack_minimax_h3_qkv,
