@@ -72,6 +72,7 @@ def test_generic_forward_head_dims_on_token_grids(native, head_dim, grid, first_
 
 
 @pytest.mark.parametrize("head_dim,dtype,tokens,exact", [
+    (8, torch.bfloat16, 300, 1),      # padded 64, one 8-dim piece per slice
     (40, torch.float16, 1000, 2),     # padded 64
     (64, torch.bfloat16, 1024, 2),
     (96, torch.bfloat16, 900, 3),
