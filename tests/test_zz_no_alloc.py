@@ -25,25 +25,25 @@ def lib():
     return _lib
 
 
-def _qkv(batch, heads, tokens, seed):
+def _qkv(batch, heads, tokens, seed, dim=D):
     gen = torch.Generator().manual_seed(seed)
-    storage = [(0.5 * torch.randn((batch, tokens, heads, D), generator=gen)).to(torch.bfloat16).cuda()
+    storage = [(0.5 * torch.randn((batch, tokens, heads, dim), generator=gen)).to(torch.bfloat16).cuda()
                for _ in range(3)]
     return [t.permute(0, 2, 1, 3) for t in storage]  # BHTD views of [B,T,H,D] storage
 
 
 def _args(lib, q, k, v, out, grid, exact, stats, route, first_order):
-    batch, heads, tokens, _ = q.shape
-    return (lib.DTYPE_BF16, batch, heads, tokens, D, lib.view4(q), lib.view4(k), lib.view4(v), lib.view4(out),
-            lib.grid(*grid), exact, 1.0 / math.sqrt(D), lib.NO_SINK, stats, route, first_order)
+    batch, heads, tokens, dim = q.shape
+    return (lib.DTYPE_BF16, batch, heads, tokens, dim, lib.view4(q), lib.view4(k), lib.view4(v), lib.view4(out),
+            lib.grid(*grid), exact, 1.0 / math.sqrt(dim), lib.NO_SINK, stats, route, first_order)
 
 
 def _both(lib, q, k, v, grid, exact, stats, route, first_order):
-    batch, heads, tokens, _ = q.shape
+    batch, heads, tokens, dim = q.shape
     stream = torch.cuda.current_stream().cuda_stream
-    out_ws = torch.empty((batch, heads, tokens, D), dtype=torch.bfloat16, device="cuda")
+    out_ws = torch.empty((batch, heads, tokens, dim), dtype=torch.bfloat16, device="cuda")
     out_static = torch.full_like(out_ws, float("nan"))
-    need = lib.LIB.pisa_hip_forward_workspace_bytes(batch, heads, tokens, D, exact)
+    need = lib.LIB.pisa_hip_forward_workspace_bytes(batch, heads, tokens, dim, exact)
     workspace = torch.empty(need, dtype=torch.uint8, device="cuda")
     lib.check(lib.LIB.pisa_hip_forward(*_args(lib, q, k, v, out_ws, grid, exact, stats, route, first_order),
                                        None, None, workspace.data_ptr(), need, stream), "pisa_hip_forward")
@@ -62,6 +62,11 @@ def test_noalloc_equals_the_workspace_entry_point_on_two_calls(lib):
     # call 2: a smaller generic problem right after (the scratch holds call 1's tables)
     q, k, v = _qkv(1, 3, 4096, seed=8)
     ref, got = _both(lib, q, k, v, (1, 64, 64), 10, lib.STATS_GENERIC, lib.ROUTE_CENTROID, 1)
+    assert torch.isfinite(ref).all()
+    assert torch.equal(ref, got)
+    # call 3: head dim 64 with the first-order term (H_sum partials of the covariance kernel in the scratch)
+    q, k, v = _qkv(2, 2, 1000, seed=9, dim=64)
+    ref, got = _both(lib, q, k, v, (0, 0, 0), 3, lib.STATS_GENERIC, lib.ROUTE_CENTROID, 1)
     assert torch.isfinite(ref).all()
     assert torch.equal(ref, got)
 
