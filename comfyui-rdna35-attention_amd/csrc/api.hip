@@ -358,14 +358,14 @@ static int prepare_impl(int32_t dtype, int32_t heads, int32_t tokens, int32_t he
     int rc;
     if (head_dim != 128) {
         const int padded = pisa::padded_head_dim(head_dim);
-        if ((rc = pisa::launch_stats_means(dtype, padded, sa, bh, st))) return rc;
+        if ((rc = pisa::launch_stats_means(dtype, padded, sa, bh, st, false))) return rc;
         if ((rc = pisa::launch_kv_pack(dtype, padded, head_dim, sa.k, sa.v, sa.map, tokens, p.blocks, bh,
                                        static_cast<char*>(w.kp), static_cast<char*>(w.vp), st)))
             return rc;
         if (first_order) {
             // H_sum of the Triton statistics (pisa_kernel.py:80-84) from the
             // block means just written, then dtype(H_sum)^T for the correction
-            pisa::CovArgs ca;
+            pisa::CovArgs ca{};
             ca.k = sa.k;
             ca.v = sa.v;
             ca.map = sa.map;
@@ -375,7 +375,7 @@ static int prepare_impl(int32_t dtype, int32_t heads, int32_t tokens, int32_t he
             plan_cov(bh, p.blocks, padded, &ca.chunks, &ca.chunk_blocks);
             ca.kmean = w.kc;
             ca.hpart = w.hpart;
-            if ((rc = pisa::launch_stats_cov(dtype, padded, ca, bh, st))) return rc;
+            if ((rc = pisa::launch_stats_cov(dtype, padded, ca, bh, st, false))) return rc;
             pisa::ReduceArgs cr{};
             cr.hpart = w.hpart;
             cr.chunks = ca.chunks;
@@ -574,15 +574,22 @@ int pisa_hip_forward_noalloc(int32_t dtype, int32_t batch, int32_t heads, int32_
                             PISA_NOALLOC_SCRATCH_BYTES, stream);
 }
 
+// Head dims other than 128: the H_sum partials of plan_cov's chunks, then the
+// per-block tile sums of squares of H_b that the norms are reduced from.
+static int64_t cov_partial_bytes(int bh, int blocks, int padded) {
+    int chunks, chunk_blocks;
+    plan_cov(bh, blocks, padded, &chunks, &chunk_blocks);
+    return ((int64_t)bh * chunks * padded * padded * 4 + 255) / 256 * 256;
+}
+
 int64_t pisa_hip_block_stats_workspace_bytes(int32_t batch, int32_t heads, int32_t tokens, int32_t head_dim) {
     if (batch <= 0 || heads <= 0 || tokens <= 0 || head_dim <= 0) return 0;
     const StatsPlan p = plan_stats(batch * heads, tokens);
     if (head_dim == 128) return (int64_t)batch * heads * p.chunks * head_dim * head_dim * 4;
     const int padded = pisa::padded_head_dim(head_dim);
     if (!padded) return 0;
-    int chunks, chunk_blocks;
-    plan_cov(batch * heads, p.blocks, padded, &chunks, &chunk_blocks);
-    return (int64_t)batch * heads * chunks * padded * padded * 4;
+    const int tiles = (padded / 32) * (padded / 32);
+    return cov_partial_bytes(batch * heads, p.blocks, padded) + (int64_t)batch * heads * p.blocks * tiles * 4;
 }
 
 int pisa_hip_block_stats(int32_t dtype, int32_t out_dtype, int32_t batch, int32_t heads, int32_t tokens,
@@ -595,21 +602,19 @@ int pisa_hip_block_stats(int32_t dtype, int32_t out_dtype, int32_t batch, int32_
     if (batch <= 0 || heads <= 0 || tokens <= 0) return fail(PISA_ERR_INVALID_ARGUMENT, "requires B>0, H>0, T>0");
     if (stats_mode != PISA_STATS_MEANS && stats_mode != PISA_STATS_HYD && stats_mode != PISA_STATS_GENERIC)
         return fail(PISA_ERR_INVALID_ARGUMENT, "unknown stats_mode %d", stats_mode);
-    // head dims other than 128: the Triton statistics of pisa_kernel.py:90-130
-    // (any width up to 256, no H_b norms), here at multiples of 8
+    // head dims other than 128: the HYD statistics (block_stats_hyd takes any
+    // 0 < D <= 256, pisa_kernels.cu:603) and the Triton statistics
+    // (pisa_kernel.py:90-130, any width up to 256), here at multiples of 8
     const int padded = head_dim == 128 ? 128 : pisa::padded_head_dim(head_dim);
-    if (head_dim != 128) {
-        if (!padded)
-            return fail(PISA_ERR_UNSUPPORTED, "block statistics support head_dim a multiple of 8 up to 256, got %d",
-                        head_dim);
-        if (stats_mode == PISA_STATS_HYD)
-            return fail(PISA_ERR_UNSUPPORTED, "HYD statistics require head_dim=128, got %d", head_dim);
-        if (h_norm) return fail(PISA_ERR_INVALID_ARGUMENT, "h_norm is formed at head_dim=128 only (pass null)");
-    }
+    if (head_dim != 128 && !padded)
+        return fail(PISA_ERR_UNSUPPORTED, "block statistics support head_dim a multiple of 8 up to 256, got %d",
+                    head_dim);
     if (!q_centroids || !k_centroids || !v_means) return fail(PISA_ERR_INVALID_ARGUMENT, "centroid outputs are required");
     const bool cov = stats_mode != PISA_STATS_MEANS;
-    if (cov && (!h_sum || (head_dim == 128 && !h_norm)))
-        return fail(PISA_ERR_INVALID_ARGUMENT, head_dim == 128 ? "h_sum and h_norm are required" : "h_sum is required");
+    // h_norm: required for HYD; optional for GENERIC off 128 (the Triton
+    // statistics form no norms), required at 128 where the kernel writes them
+    if (cov && (!h_sum || (!h_norm && (stats_mode == PISA_STATS_HYD || head_dim == 128))))
+        return fail(PISA_ERR_INVALID_ARGUMENT, "h_sum and h_norm are required");
     int rc;
     if ((rc = check_grid(grid, tokens)) || (rc = check_view("q", q, 2, true)) || (rc = check_view("k", k, 2, true)) ||
         (rc = check_view("v", v, 2, true)))
@@ -642,9 +647,10 @@ int pisa_hip_block_stats(int32_t dtype, int32_t out_dtype, int32_t batch, int32_
     sa.npad = p.npad;
     sa.head_dim = head_dim;
     if (head_dim != 128) {
-        if ((rc = pisa::launch_stats_means(dtype, padded, sa, bh, st))) return rc;
+        const bool hyd = stats_mode == PISA_STATS_HYD;
+        if ((rc = pisa::launch_stats_means(dtype, padded, sa, bh, st, hyd))) return rc;
         if (!cov) return PISA_OK;
-        pisa::CovArgs ca;
+        pisa::CovArgs ca{};
         ca.k = sa.k;
         ca.v = sa.v;
         ca.map = sa.map;
@@ -654,7 +660,10 @@ int pisa_hip_block_stats(int32_t dtype, int32_t out_dtype, int32_t batch, int32_
         plan_cov(bh, p.blocks, padded, &ca.chunks, &ca.chunk_blocks);
         ca.kmean = k_centroids;
         ca.hpart = static_cast<float*>(workspace);
-        if ((rc = pisa::launch_stats_cov(dtype, padded, ca, bh, st))) return rc;
+        ca.normpart = h_norm ? reinterpret_cast<float*>(static_cast<char*>(workspace) +
+                                                        cov_partial_bytes(bh, p.blocks, padded))
+                             : nullptr;
+        if ((rc = pisa::launch_stats_cov(dtype, padded, ca, bh, st, hyd))) return rc;
         pisa::ReduceArgs cr{};
         cr.hpart = ca.hpart;
         cr.chunks = ca.chunks;
@@ -662,6 +671,8 @@ int pisa_hip_block_stats(int32_t dtype, int32_t out_dtype, int32_t batch, int32_
         cr.hsum_dim = head_dim;
         cr.blocks = p.blocks;
         cr.npad = p.npad;
+        cr.normpart = ca.normpart;
+        cr.hnorm = h_norm;
         return pisa::launch_cov_reduce(dtype, padded, cr, bh, st);
     }
     if ((rc = pisa::launch_stats(dtype, stats_mode, sa, bh, st))) return rc;

@@ -43,6 +43,10 @@ struct ReduceArgs {
     void* kbar_pad;    // nullable
     void* vbar_t_pad;  // nullable
     int blocks, npad;
+    // head dims other than 128: per-block tile sums of squares of H_b
+    // ([BH][N][tiles], from stats_cov_kernel) and ||H_b||_F out (both nullable)
+    const float* normpart;
+    float* hnorm;
 };
 
 // One 32x32 tile (tile = (D/32) * row tile + column tile) of the H_sum
@@ -165,19 +169,21 @@ struct LayoutArgs {
 };
 
 int launch_stats(int dtype, int mode, const StatsArgs& a, int bh_count, hipStream_t stream);
-// H_sum partials of the generic statistics at a padded head dim other than 128
-// (the statistics kernel forms them at 128): H_b = dtype(K_b - k_bar_b)^T V_b
-// summed over each chunk of chunk_blocks blocks, one wave per (head, chunk,
-// 32x32 tile of H).  kmean holds the fp32 block means of K that the means
-// kernel wrote ([BH][N][head_dim]).
+// H_sum partials at a padded head dim other than 128 (the statistics kernel
+// forms them at 128): H_b = (K_b - k_bar_b)^T V_b summed over each chunk of
+// chunk_blocks blocks, one wave per (head, chunk, 32x32 tile of H); centred
+// keys rounded to the dtype (generic) or kept at fp32 accuracy (hyd).  kmean
+// holds the fp32 block means of K that the means kernel wrote
+// ([BH][N][head_dim]).
 struct CovArgs {
     View k, v;
     TokenMap map;
     int tokens, blocks, head_dim, chunk_blocks, chunks;
     const float* kmean;
-    float* hpart;  // [BH][chunks][Dp][Dp]
+    float* hpart;     // [BH][chunks][Dp][Dp]
+    float* normpart;  // [BH][N][(Dp/32)^2] tile sums of squares of H_b (nullable)
 };
-int launch_stats_cov(int dtype, int padded, const CovArgs& a, int bh_count, hipStream_t stream);
+int launch_stats_cov(int dtype, int padded, const CovArgs& a, int bh_count, hipStream_t stream, bool hyd);
 // Chunk-order sum of launch_stats_cov's partials into dtype(H_sum)^T packed at
 // the padded width (ReduceArgs.ht; hsum optional).
 int launch_cov_reduce(int dtype, int padded, const ReduceArgs& a, int bh_count, hipStream_t stream);
@@ -186,8 +192,9 @@ int launch_route(const RouteArgs& a, hipStream_t stream);
 // Routing with the H_sum reduction of head dim 128 (stats_reduce_kernel's work,
 // `r`) done by the routing workgroups of each head before they score.
 int launch_route_reduce(int dtype, const RouteArgs& a, const ReduceArgs& r, hipStream_t stream);
-// Block means for the generic path at padded width `padded` (a.head_dim < 128 or > 128).
-int launch_stats_means(int dtype, int padded, const StatsArgs& a, int bh_count, hipStream_t stream);
+// Block means at padded width `padded` (a.head_dim < 128 or > 128): sum / len,
+// or sum * (1/len) for the HYD statistics (`hyd`).
+int launch_stats_means(int dtype, int padded, const StatsArgs& a, int bh_count, hipStream_t stream, bool hyd);
 // `padded` = padded_head_dim(a.head_dim); dense (sparse = tail = false) or PISA (both true).
 int launch_attention(int dtype, int padded, bool sparse, bool tail, const AttnArgs& a, int bh_count,
                      hipStream_t stream);

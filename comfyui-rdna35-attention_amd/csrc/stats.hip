@@ -320,15 +320,17 @@ __global__ __launch_bounds__(256) void stats_reduce_kernel(ReduceArgs a) {
     if (blockIdx.x == 0) zero_centroid_pad<T>(a, blockIdx.y, threadIdx.x);
 }
 
-// Block means of the generic path at head dims other than 128 (H_sum, when
-// the first-order term is asked for, comes from stats_cov_kernel below): one
-// 256-thread workgroup per (batch*head, block).
+// Block means at head dims other than 128 (H_sum and the H_b norms, when
+// asked for, come from stats_cov_kernel below): one 256-thread workgroup per
+// (batch*head, block).
 // Thread (row group rr, piece pc) sums the 8 dims pc*8.. of rows rr, rr+R, ..
-// in fp32; an LDS pass adds the R row groups in order, and means are
-// sum / len (generic_pisa.py:128-132, pisa_kernel.py:72-77).  Writes the
-// [BH][N][D] means and the packed centroid chunks at the padded width DP
-// (zero in dims >= D and for the centroids past the last block).
-template <typename T, int DP>
+// in fp32; an LDS pass adds the R row groups in order.  Means are sum / len
+// for the generic statistics (generic_pisa.py:128-132, pisa_kernel.py:72-77)
+// and sum * fp32(1/len) for the HYD statistics (pisa_kernels.cu:207-209).
+// Writes the [BH][N][D] means and, for the attention kernel, the packed
+// centroid chunks at the padded width DP (zero in dims >= D and for the
+// centroids past the last block).
+template <typename T, int DP, bool HYD>
 __global__ __launch_bounds__(256) void stats_means_kernel(StatsArgs a) {
     typedef typename Elem<T>::vec8 vec8;
     constexpr int P = DP / 8;    // 16-byte pieces per row
@@ -384,9 +386,16 @@ __global__ __launch_bounds__(256) void stats_means_kernel(StatsArgs a) {
         mv += red[2][i][d];
     }
     const float fl = static_cast<float>(len);
-    mq /= fl;
-    mk /= fl;
-    mv /= fl;
+    if (HYD) {
+        const float inv_len = 1.0f / fl;
+        mq *= inv_len;
+        mk *= inv_len;
+        mv *= inv_len;
+    } else {
+        mq /= fl;
+        mk /= fl;
+        mv /= fl;
+    }
     const bool live = d < a.head_dim;
     if (live) {
         const int64_t o = ((int64_t)bh * a.blocks + b) * a.head_dim + d;
@@ -415,45 +424,56 @@ __global__ __launch_bounds__(256) void stats_means_kernel(StatsArgs a) {
     }
 }
 
-template <typename T>
+template <typename T, bool HYD>
 int launch_stats_means_t(int padded, const StatsArgs& a, int bh_count, hipStream_t stream) {
     const dim3 grid(bh_count * a.blocks);
     switch (padded) {
-        case 64: hipLaunchKernelGGL((stats_means_kernel<T, 64>), grid, dim3(256), 0, stream, a); break;
-        case 96: hipLaunchKernelGGL((stats_means_kernel<T, 96>), grid, dim3(256), 0, stream, a); break;
-        case 128: hipLaunchKernelGGL((stats_means_kernel<T, 128>), grid, dim3(256), 0, stream, a); break;  // 104..120
-        case 160: hipLaunchKernelGGL((stats_means_kernel<T, 160>), grid, dim3(256), 0, stream, a); break;
-        case 192: hipLaunchKernelGGL((stats_means_kernel<T, 192>), grid, dim3(256), 0, stream, a); break;
-        case 256: hipLaunchKernelGGL((stats_means_kernel<T, 256>), grid, dim3(256), 0, stream, a); break;
+        case 64: hipLaunchKernelGGL((stats_means_kernel<T, 64, HYD>), grid, dim3(256), 0, stream, a); break;
+        case 96: hipLaunchKernelGGL((stats_means_kernel<T, 96, HYD>), grid, dim3(256), 0, stream, a); break;
+        case 128: hipLaunchKernelGGL((stats_means_kernel<T, 128, HYD>), grid, dim3(256), 0, stream, a); break;  // 104..120
+        case 160: hipLaunchKernelGGL((stats_means_kernel<T, 160, HYD>), grid, dim3(256), 0, stream, a); break;
+        case 192: hipLaunchKernelGGL((stats_means_kernel<T, 192, HYD>), grid, dim3(256), 0, stream, a); break;
+        case 256: hipLaunchKernelGGL((stats_means_kernel<T, 256, HYD>), grid, dim3(256), 0, stream, a); break;
         default: return pisa_host::fail(PISA_ERR_UNSUPPORTED, "block means: padded head dim %d", padded);
     }
     return pisa_host::check_launch("stats_means_kernel");
 }
 
-int launch_stats_means(int dtype, int padded, const StatsArgs& a, int bh_count, hipStream_t stream) {
-    if (dtype == PISA_DTYPE_BF16) return launch_stats_means_t<bf16_t>(padded, a, bh_count, stream);
-    return launch_stats_means_t<f16_t>(padded, a, bh_count, stream);
+int launch_stats_means(int dtype, int padded, const StatsArgs& a, int bh_count, hipStream_t stream, bool hyd) {
+    if (dtype == PISA_DTYPE_BF16)
+        return hyd ? launch_stats_means_t<bf16_t, true>(padded, a, bh_count, stream)
+                   : launch_stats_means_t<bf16_t, false>(padded, a, bh_count, stream);
+    return hyd ? launch_stats_means_t<f16_t, true>(padded, a, bh_count, stream)
+               : launch_stats_means_t<f16_t, false>(padded, a, bh_count, stream);
 }
 
-// H_sum partials of the generic statistics for head dims other than 128
-// (pisa_kernel.py:71-84, the Triton statistics every head dim up to 256 takes:
-// centred keys rounded to the input dtype, H_b = centred^T V accumulated in
-// fp32).  One wave per (head, chunk of blocks, 32x32 tile (tr, tc) of H): for
-// each block it reads the block's 32 key dims of row slice tr and 32 value dims
-// of column slice tc (16-byte pieces, token order from the grid map), centres
-// the keys on the fp32 means of the means kernel, stages both slices transposed
-// in LDS (dim-major, 4 consecutive tokens per 8-byte write) and accumulates
-// H[32tr + i][32tc + j] with four 32x32x16 MFMAs (tokens as the contraction).
-// Rows past a short last block contribute zero, as their zero values make
-// them contribute in the reference.  The partial of each chunk is written once
-// (no float atomics; the reference adds with tl.atomic_add).
-template <typename T, int DP>
+// H_sum partials (and H_b norms) at head dims other than 128, one wave per
+// (head, chunk of blocks, 32x32 tile (tr, tc) of H).  For each block it reads
+// the block's 32 key dims of row slice tr and 32 value dims of column slice tc
+// (16-byte pieces, token order from the grid map), centres the keys on the
+// fp32 block means of the means kernel, stages both slices transposed in LDS
+// (dim-major, 4 consecutive tokens per 8-byte write) and forms the tile
+// H_b[32tr + i][32tc + j] with 32x32x16 MFMAs (tokens as the contraction),
+// which it adds to the chunk's partial.
+//   HYD = false: the Triton statistics every head dim up to 256 takes
+//     (pisa_kernel.py:71-84): centred keys rounded to the input dtype.
+//   HYD = true: block_stats_hyd_kernel (pisa_kernels.cu:214-243): keys
+//     centred in fp32, carried as a dtype pair hi + lo (hi = dtype(c),
+//     lo = dtype(c - hi)) with one MFMA pass each.
+// When normpart is set, the wave also writes the tile's sum of squares of
+// H_b for every block ([BH][N][tiles]); cov_reduce_kernel adds the tiles in
+// order into ||H_b||_F.  Rows past a short last block contribute zero, as
+// their zero values make them contribute in the reference.  The partial of
+// each chunk is written once (no float atomics; the reference adds with
+// atomicAdd / tl.atomic_add).
+template <typename T, int DP, bool HYD>
 __global__ __launch_bounds__(64) void stats_cov_kernel(CovArgs a) {
     typedef typename Elem<T>::vec8 vec8;
     typedef T vec4 __attribute__((ext_vector_type(4)));
     constexpr int TD = DP / 32;
     constexpr int kRowT = kBlock + 8;  // padded LDS row (tokens) of a transposed slice
     __shared__ __attribute__((aligned(16))) T kts[32 * kRowT];
+    __shared__ __attribute__((aligned(16))) T kts_lo[HYD ? 32 * kRowT : 8];
     __shared__ __attribute__((aligned(16))) T vts[32 * kRowT];
     const int lane = threadIdx.x;
     const int tile = blockIdx.x % (TD * TD);
@@ -489,24 +509,48 @@ __global__ __launch_bounds__(64) void stats_cov_kernel(CovArgs a) {
             if (kdims) kx[r] = load8<vec8>(a.k.data + (a.k.row(bh, raster) + dk) * (int64_t)sizeof(T));
             if (vdims) vx[r] = load8<vec8>(a.v.data + (a.v.row(bh, raster) + dv) * (int64_t)sizeof(T));
         }
+        // the previous block's operand reads by other lanes come before these
+        // stores (one wave: the barrier orders its LDS accesses, at no cost)
+        __syncthreads();
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            vec4 ck, cv;
+            vec4 ck, cl, cv;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const bool valid = 4 * q4 + r < len;
-                ck[r] = (valid && kdims) ? from_f32<T>(to_f32(kx[r][e]) - mean[e]) : T(0.0f);
+                const float c = (valid && kdims) ? to_f32(kx[r][e]) - mean[e] : 0.0f;
+                ck[r] = from_f32<T>(c);
+                if (HYD) cl[r] = from_f32<T>(c - to_f32(ck[r]));
                 cv[r] = (valid && vdims) ? vx[r][e] : T(0.0f);
             }
             *reinterpret_cast<vec4*>(&kts[(8 * pc + e) * kRowT + 4 * q4]) = ck;
+            if (HYD) *reinterpret_cast<vec4*>(&kts_lo[(8 * pc + e) * kRowT + 4 * q4]) = cl;
             *reinterpret_cast<vec4*>(&vts[(8 * pc + e) * kRowT + 4 * q4]) = cv;
         }
-        // one wave: its LDS writes and reads stay in program order
+        // the slices written by every lane are read below
+        __syncthreads();
+        f32x16 hb;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) hb[v] = 0.0f;
 #pragma unroll
         for (int st = 0; st < 4; ++st) {
             const vec8 ka = *reinterpret_cast<const vec8*>(&kts[col * kRowT + 16 * st + 8 * half]);
             const vec8 vb = *reinterpret_cast<const vec8*>(&vts[col * kRowT + 16 * st + 8 * half]);
-            acc = mfma32(ka, vb, acc);
+            hb = mfma32(ka, vb, hb);
+            if (HYD) {
+                const vec8 kl = *reinterpret_cast<const vec8*>(&kts_lo[col * kRowT + 16 * st + 8 * half]);
+                hb = mfma32(kl, vb, hb);
+            }
+        }
+        float ss = 0.0f;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            acc[v] += hb[v];
+            ss += hb[v] * hb[v];
+        }
+        if (a.normpart) {
+            ss = wave_sum(ss);
+            if (lane == 0) a.normpart[((int64_t)bh * a.blocks + b) * (TD * TD) + tile] = ss;
         }
     }
     float* dst = a.hpart + ((int64_t)bh * a.chunks + chunk) * DP * DP;
@@ -517,42 +561,59 @@ __global__ __launch_bounds__(64) void stats_cov_kernel(CovArgs a) {
     }
 }
 
+// Chunk-order sum of the partials (one 32x32 tile of H_sum per workgroup);
+// the tile-0 workgroup of each head also adds every block's tile sums of
+// squares in tile order into ||H_b||_F when asked for.
 template <typename T, int DP>
 __global__ __launch_bounds__(256) void cov_reduce_kernel(ReduceArgs a) {
     __shared__ float tile[32][33];
-    reduce_h_tile<T, DP>(a, blockIdx.y, blockIdx.x, tile, threadIdx.x);
+    const int bh = blockIdx.y;
+    reduce_h_tile<T, DP>(a, bh, blockIdx.x, tile, threadIdx.x);
+    if (blockIdx.x == 0 && a.hnorm) {
+        constexpr int kTiles = (DP / 32) * (DP / 32);
+        for (int b = threadIdx.x; b < a.blocks; b += 256) {
+            const float* src = a.normpart + ((int64_t)bh * a.blocks + b) * kTiles;
+            float ss = 0.0f;
+#pragma unroll 8
+            for (int i = 0; i < kTiles; ++i) ss += src[i];
+            a.hnorm[(int64_t)bh * a.blocks + b] = sqrtf(ss);
+        }
+    }
 }
 
 template <typename T, int DP>
-static void launch_cov_dp(const CovArgs& a, const ReduceArgs* r, int bh_count, hipStream_t stream) {
+static void launch_cov_dp(const CovArgs& a, const ReduceArgs* r, bool hyd, int bh_count, hipStream_t stream) {
     constexpr int tiles = (DP / 32) * (DP / 32);
+    const dim3 grid(bh_count * a.chunks * tiles);
     if (r) hipLaunchKernelGGL((cov_reduce_kernel<T, DP>), dim3(tiles, bh_count), dim3(256), 0, stream, *r);
-    else hipLaunchKernelGGL((stats_cov_kernel<T, DP>), dim3(bh_count * a.chunks * tiles), dim3(64), 0, stream, a);
+    else if (hyd) hipLaunchKernelGGL((stats_cov_kernel<T, DP, true>), grid, dim3(64), 0, stream, a);
+    else hipLaunchKernelGGL((stats_cov_kernel<T, DP, false>), grid, dim3(64), 0, stream, a);
 }
 
 template <typename T>
-static int launch_cov_t(int padded, const CovArgs& a, const ReduceArgs* r, int bh_count, hipStream_t stream) {
+static int launch_cov_t(int padded, const CovArgs& a, const ReduceArgs* r, bool hyd, int bh_count,
+                        hipStream_t stream) {
     switch (padded) {
-        case 64: launch_cov_dp<T, 64>(a, r, bh_count, stream); break;
-        case 96: launch_cov_dp<T, 96>(a, r, bh_count, stream); break;
-        case 128: launch_cov_dp<T, 128>(a, r, bh_count, stream); break;  // head dims 104..120
-        case 160: launch_cov_dp<T, 160>(a, r, bh_count, stream); break;
-        case 192: launch_cov_dp<T, 192>(a, r, bh_count, stream); break;
-        case 256: launch_cov_dp<T, 256>(a, r, bh_count, stream); break;
+        case 64: launch_cov_dp<T, 64>(a, r, hyd, bh_count, stream); break;
+        case 96: launch_cov_dp<T, 96>(a, r, hyd, bh_count, stream); break;
+        case 128: launch_cov_dp<T, 128>(a, r, hyd, bh_count, stream); break;  // head dims 104..120
+        case 160: launch_cov_dp<T, 160>(a, r, hyd, bh_count, stream); break;
+        case 192: launch_cov_dp<T, 192>(a, r, hyd, bh_count, stream); break;
+        case 256: launch_cov_dp<T, 256>(a, r, hyd, bh_count, stream); break;
         default: return pisa_host::fail(PISA_ERR_UNSUPPORTED, "H_sum: padded head dim %d", padded);
     }
     return pisa_host::check_launch(r ? "cov_reduce_kernel" : "stats_cov_kernel");
 }
 
-int launch_stats_cov(int dtype, int padded, const CovArgs& a, int bh_count, hipStream_t stream) {
-    if (dtype == PISA_DTYPE_BF16) return launch_cov_t<bf16_t>(padded, a, nullptr, bh_count, stream);
-    return launch_cov_t<f16_t>(padded, a, nullptr, bh_count, stream);
+int launch_stats_cov(int dtype, int padded, const CovArgs& a, int bh_count, hipStream_t stream, bool hyd) {
+    if (dtype == PISA_DTYPE_BF16) return launch_cov_t<bf16_t>(padded, a, nullptr, hyd, bh_count, stream);
+    return launch_cov_t<f16_t>(padded, a, nullptr, hyd, bh_count, stream);
 }
 
 int launch_cov_reduce(int dtype, int padded, const ReduceArgs& r, int bh_count, hipStream_t stream) {
     const CovArgs none{};
-    if (dtype == PISA_DTYPE_BF16) return launch_cov_t<bf16_t>(padded, none, &r, bh_count, stream);
-    return launch_cov_t<f16_t>(padded, none, &r, bh_count, stream);
+    if (dtype == PISA_DTYPE_BF16) return launch_cov_t<bf16_t>(padded, none, &r, false, bh_count, stream);
+    return launch_cov_t<f16_t>(padded, none, &r, false, bh_count, stream);
 }
 
 template <typename T, int MODE>

@@ -378,8 +378,9 @@ def _fixed_block_op_fake(q, k, v, scale, causal, mask):
 
 # --------------------------------------------------------------------------- statistics
 def _block_stats(q, k, v, mode, out_dtype):
-    """q/k/v: [BH,T,D] (or [B,H,T,D] views).  Returns the 5 HYD outputs (3 for MEANS); at head dims other than
-    128 (GENERIC or MEANS statistics) h_norm is None."""
+    """q/k/v: [BH,T,D] (or [B,H,T,D] views).  Returns the 5 HYD outputs (3 for MEANS); h_norm is formed at every
+    head dim for HYD statistics and is None for GENERIC statistics off head dim 128 (the Triton statistics form
+    no norms)."""
     q4 = q if q.ndim == 4 else _as4(q)
     k4 = k if k.ndim == 4 else _as4(k)
     v4 = v if v.ndim == 4 else _as4(v)
@@ -392,7 +393,8 @@ def _block_stats(q, k, v, mode, out_dtype):
     v_means = q.new_empty(shape, dtype=out_dtype)
     cov = mode != _lib.STATS_MEANS
     h_sum = q.new_empty((bh, head_dim, head_dim), dtype=torch.float32) if cov else None
-    h_norm = q.new_empty((bh, blocks), dtype=torch.float32) if cov and head_dim == HEAD_DIM else None  # 128 only
+    with_norm = cov and (mode == _lib.STATS_HYD or head_dim == HEAD_DIM)
+    h_norm = q.new_empty((bh, blocks), dtype=torch.float32) if with_norm else None
     with on_device(q.device):
         ws_bytes = LIB.pisa_hip_block_stats_workspace_bytes(batch, heads, tokens, head_dim) if cov else 0
         workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
@@ -410,12 +412,18 @@ def _block_stats(q, k, v, mode, out_dtype):
     return q_centroids, k_centroids, v_means, h_sum, h_norm
 
 
+HYD_STATS_HEAD_DIMS = GENERIC_HEAD_DIMS  # block_stats_hyd: 0<D<=256 in the reference, multiples of 8 here
+
+
 def block_stats_hyd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor):
-    """(q_bar, k_bar fp32, v_bar, H_sum fp32) of [BH,T,D] q/k/v (__init__.py:216-230)."""
+    """(q_bar, k_bar fp32, v_bar, H_sum fp32) of [BH,T,D] q/k/v (__init__.py:216-230).
+
+    Any head dim that is a multiple of 8 up to 256 (the reference takes any 0<D<=256), fp16 or bf16.
+    """
     if q.ndim != 3 or q.shape != k.shape or q.shape != v.shape:
         raise ValueError("PISA HIP HYD expects matching [BH,T,D] q/k/v tensors.")
-    if q.shape[0] <= 0 or q.shape[1] <= 0 or q.shape[1] > MAX_TOKENS or q.shape[2] != HEAD_DIM:
-        raise ValueError(f"PISA HIP HYD requires BH>0, 0<T<={MAX_TOKENS}, and D={HEAD_DIM}.")
+    if q.shape[0] <= 0 or q.shape[1] <= 0 or q.shape[1] > MAX_TOKENS or q.shape[2] not in HYD_STATS_HEAD_DIMS:
+        raise ValueError(f"PISA HIP HYD requires BH>0, 0<T<={MAX_TOKENS}, and 0<D<=256 with D a multiple of 8.")
     if q.device != k.device or q.device != v.device or not _is_rocm_device(q):
         raise ValueError("PISA HIP HYD requires q/k/v on one PyTorch ROCm device.")
     if q.dtype not in (torch.float16, torch.bfloat16) or k.dtype != q.dtype or v.dtype != q.dtype:
@@ -691,8 +699,14 @@ def capabilities() -> dict[str, object]:
         "spatial_bhtd": True,
         "spatial_tokens": SPATIAL_TOKENS,
         "spatial_sparse_exact_blocks": (SPATIAL_SPARSE_EXACT_BLOCKS,),
+        # where the generic path routes on HYD statistics (generic_stats_mode; the reference's
+        # _block_stats reads these two keys, generic_pisa.py:123-124) ...
         "hyd_stats_head_dims": (HEAD_DIM,),
-        "hyd_stats_dtypes": (torch.bfloat16, torch.float16),
+        "hyd_stats_dtypes": (torch.bfloat16,),
+        # ... and what block_stats_hyd itself accepts
+        "block_stats_hyd_head_dims": HYD_STATS_HEAD_DIMS,
+        "block_stats_hyd_dtypes": (torch.bfloat16, torch.float16),
+        "block_stats_hyd_max_tokens": MAX_TOKENS,
         "generic_head_dims": GENERIC_HEAD_DIMS,
         "generic_dtypes": (torch.bfloat16, torch.float16),
         "dense_head_dims": GENERIC_HEAD_DIMS,
@@ -741,24 +755,29 @@ class _NativeNamespace:
         return build_info()
 
     @staticmethod
-    def _stats_inputs(q, k, v):
+    def _stats_inputs(q, k, v, head_dims, max_tokens=MAX_TOKENS):
         if not all(isinstance(t, torch.Tensor) for t in (q, k, v)) or q.ndim != 3:
             raise RuntimeError("block statistics expect matching [BH,T,D] q/k/v.")
         for name, tensor in (("q", q), ("k", k), ("v", v)):
             _check_native(name, tensor, tuple(q.shape), (torch.bfloat16, torch.float16), q.device)
         if k.dtype != q.dtype or v.dtype != q.dtype:
             raise RuntimeError("q, k, and v must have the same dtype.")
-        if q.shape[2] != HEAD_DIM or q.shape[0] <= 0 or q.shape[1] <= 0 or q.shape[1] > MAX_TOKENS:
-            raise RuntimeError(f"block statistics require BH>0, 0<T<={MAX_TOKENS}, and D={HEAD_DIM}.")
+        if q.shape[0] <= 0 or q.shape[1] <= 0 or q.shape[2] not in head_dims:
+            dims = f"D={HEAD_DIM}" if tuple(head_dims) == (HEAD_DIM,) else "0<D<=256 with D a multiple of 8"
+            raise RuntimeError(f"block statistics require BH>0, T>0, and {dims}.")
+        if q.shape[1] > max_tokens:
+            raise RuntimeError(f"block statistics support T<={max_tokens}.")
 
     @staticmethod
     def block_stats(q, k, v):
-        _NativeNamespace._stats_inputs(q, k, v)
+        """Plain means at D=128 (pisa_kernels.cu:563-595)."""
+        _NativeNamespace._stats_inputs(q, k, v, (HEAD_DIM,))
         return _block_stats(q, k, v, _lib.STATS_MEANS, q.dtype)
 
     @staticmethod
     def block_stats_hyd(q, k, v):
-        _NativeNamespace._stats_inputs(q, k, v)
+        """HYD statistics, all five outputs, at any head dim that is a multiple of 8 up to 256 (pisa_kernels.cu:597-635)."""
+        _NativeNamespace._stats_inputs(q, k, v, HYD_STATS_HEAD_DIMS)
         return _block_stats(q, k, v, _lib.STATS_HYD, q.dtype)
 
     @staticmethod

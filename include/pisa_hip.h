@@ -200,7 +200,10 @@ PISA_HIP_EXPORT int pisa_hip_attend(int32_t dtype, int32_t batch, int32_t heads,
  * that cannot allocate device memory (code under HIP graph capture, tight
  * serving loops, hosts that forbid hipMalloc).  The workspace is a static
  * device array of PISA_NOALLOC_SCRATCH_BYTES (256 MiB) inside the library,
- * one per GPU, held until the process ends; a problem whose
+ * one per GPU, held until the process ends.  The array belongs to the
+ * library's code object, so every process that loads libpisa_hip.so holds
+ * these 256 MiB on every GPU it uses the library on, whether or not it ever
+ * calls this entry point.  A problem whose
  * pisa_hip_forward_workspace_bytes exceeds it is refused with
  * PISA_ERR_WORKSPACE before anything is launched (the Anima profile
  * B=2 H=16 T=9216 needs 197 MB).  No debug outputs.  Every call on one GPU
@@ -229,11 +232,12 @@ PISA_HIP_EXPORT int64_t pisa_hip_block_stats_workspace_bytes(int32_t batch, int3
  *   k_centroids  [BH,N,D] float32
  *   v_means      [BH,N,D] in out_dtype
  *   h_sum        [BH,D,D] float32, nullable for PISA_STATS_MEANS
- *   h_norm       [BH,N]   float32, nullable for PISA_STATS_MEANS; null at head dims
- *                other than 128
- *   head_dim     128, or (PISA_STATS_GENERIC / PISA_STATS_MEANS) a multiple of 8 up
- *                to 256, as pisa_prepare_triton takes any width up to 256
- * H_sum is reduced deterministically (no floating-point atomics).
+ *   h_norm       [BH,N]   float32 ||H_b||_F, nullable for PISA_STATS_MEANS and, at head
+ *                dims other than 128, for PISA_STATS_GENERIC (formed when given)
+ *   head_dim     128 or any multiple of 8 up to 256, in every mode: _C.block_stats_hyd
+ *                takes 0 < D <= 256 (pisa_kernels.cu:603), pisa_prepare_triton any
+ *                width up to 256; other widths return PISA_ERR_UNSUPPORTED
+ * H_sum and h_norm are reduced deterministically (no floating-point atomics).
  */
 PISA_HIP_EXPORT int pisa_hip_block_stats(int32_t dtype, int32_t out_dtype, int32_t batch, int32_t heads,
                          int32_t tokens, int32_t head_dim, pisa_view q, pisa_view k, pisa_view v,

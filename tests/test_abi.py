@@ -121,12 +121,81 @@ def test_other_entry_points_validate(lib):
                                              None, None, None) == 1
 
 
-def test_reference_module_name_is_the_implementation():
-    """`import rdna35_pisa_ck` (the reference's native package name) yields the mi355x_pisa module."""
+def _reference_stats_choice(module, q, k, v, device_accepts: bool = False) -> str:
+    """The reference's generic statistics choice (generic_pisa.py:119-128) restated against `module`.
+
+    'hyd' when the module lists q's head dim and dtype among its HYD statistics and its block_stats_hyd
+    accepts the call, else 'generic'.  device_accepts: on CPU tensors, a refusal that names only the
+    device counts as acceptance (the shape and dtype checks come before the device check, as in
+    __init__.py:216-230), so the decision is visible without a GPU.
+    """
+    try:
+        caps = module.capabilities()
+        if q.shape[-1] in caps.get("hyd_stats_head_dims", ()) and q.dtype in caps.get("hyd_stats_dtypes", ()):
+            try:
+                module.block_stats_hyd(q, k, v)
+            except ValueError as exc:
+                if not (device_accepts and "ROCm device" in str(exc)):
+                    raise
+            return "hyd"
+    except (ImportError, OSError, RuntimeError, AttributeError, ValueError):
+        pass
+    return "generic"
+
+
+def test_reference_module_name_keeps_the_reference_contract():
+    """`import rdna35_pisa_ck` runs the mi355x_pisa kernels behind the reference's limits
+    (native/rdna35_pisa_ck/rdna35_pisa_ck/__init__.py:27-29,216-230,455-474)."""
+    import torch
+
     import mi355x_pisa
     import rdna35_pisa_ck
 
-    assert rdna35_pisa_ck is mi355x_pisa
+    assert rdna35_pisa_ck is not mi355x_pisa
     assert rdna35_pisa_ck.forward_spatial_bhtd is mi355x_pisa.forward_spatial_bhtd
-    assert rdna35_pisa_ck.capabilities()["architecture"] == "gfx950"
+    assert (rdna35_pisa_ck.MAX_BLOCKS, rdna35_pisa_ck.MAX_TOKENS) == (144, 9216)
+    caps = rdna35_pisa_ck.capabilities()
+    assert caps["architecture"] == "gfx950"
+    assert caps["max_blocks"] == 144
+    assert caps["hyd_stats_dtypes"] == (torch.bfloat16,)
+    assert caps["hyd_stats_head_dims"] == (128,)
     assert rdna35_pisa_ck.SPATIAL_SPARSE_EXACT_BLOCKS == 23
+    # the wider module agrees on the keys the reference's generic path reads
+    wide = mi355x_pisa.capabilities()
+    assert wide["hyd_stats_dtypes"] == caps["hyd_stats_dtypes"]
+    assert wide["hyd_stats_head_dims"] == caps["hyd_stats_head_dims"]
+    assert 256 in wide["block_stats_hyd_head_dims"] and torch.float16 in wide["block_stats_hyd_dtypes"]
+
+    long = torch.zeros((1, 9280, 128), dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="0<T<=9216"):
+        rdna35_pisa_ck.block_stats_hyd(long, long, long)
+    with pytest.raises(ValueError, match="0<T<=9216"):
+        rdna35_pisa_ck.forward(long, long, long, 23)
+    with pytest.raises(RuntimeError, match="T<=9216"):
+        rdna35_pisa_ck._C.block_stats_hyd(long, long, long)
+    with pytest.raises(RuntimeError, match="T<=9216"):
+        rdna35_pisa_ck._C.block_stats(long, long, long)
+    # other widths than multiples of 8 are refused with the limit named
+    odd = torch.zeros((1, 64, 100), dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="multiple of 8"):
+        mi355x_pisa.block_stats_hyd(odd, odd, odd)
+
+
+@pytest.mark.parametrize("dtype_name, tokens, head_dim", [
+    ("bfloat16", 8192, 128), ("float16", 8192, 128), ("bfloat16", 32768, 128), ("bfloat16", 9216, 128),
+    ("bfloat16", 9217, 128), ("bfloat16", 8192, 64), ("float16", 32768, 128),
+])
+def test_reference_stats_choice_through_the_alias_matches_generic_stats_mode(dtype_name, tokens, head_dim):
+    """The reference's _block_stats rule run against `rdna35_pisa_ck` picks the regime that
+    mi355x_pisa.generic_stats_mode (the HIP generic path's choice) picks."""
+    import torch
+
+    import mi355x_pisa
+    import rdna35_pisa_ck
+
+    dtype = getattr(torch, dtype_name)
+    x = torch.zeros((1, tokens, head_dim), dtype=dtype)
+    chosen = _reference_stats_choice(rdna35_pisa_ck, x, x, x, device_accepts=True)
+    assert chosen == mi355x_pisa.generic_stats_mode(tokens, head_dim, dtype)
+    expected = "hyd" if (dtype == torch.bfloat16 and head_dim == 128 and tokens <= 9216) else "generic"
+    assert chosen == expected
