@@ -11,8 +11,9 @@ tail, first-order correction, merge, raster output).
 
 Also measured in the same process, in this order:
   * the first call, reported separately (nothing is compiled at run time);
-  * 200 untimed calls: after an idle period the attention kernel runs up to
-    ~20 % slower for ~25 calls, so every region below starts at settled clocks;
+  * SETTLE_CALLS (200) untimed calls, reported as settle_calls: after an idle
+    period the attention kernel runs up to ~20 % slower for ~25 calls, so every
+    region below starts at settled clocks;
   * the metric: K whole calls after W warm-up calls;
   * the statistics + routing launches (PisaPlan.prepare) and the fused
     attention kernel alone (PisaPlan.attend, one launch), timed with HIP events
@@ -22,7 +23,9 @@ Also measured in the same process, in this order:
     correction do the same work in both), so the difference / 24 is the time
     of one exact 64-key tile step for the whole grid -> exact_tiles_marginal;
   * the dense exact attention kernel of this library on the same shape (the
-    1.8x comparator of the north star) and torch's SDPA on the same views;
+    1.8x comparator of the north star: median of per-call HIP events, with the
+    graph-replay time and host enqueue time beside it) and torch's SDPA on the
+    same views;
   * the metric's region again right after one idle second
     (call_ms_after_1s_idle);
   * the CPU baseline: the fp32 torch port of the HYD forward
@@ -77,6 +80,10 @@ METRIC = "PISA call ms + MFMA util %, bf16 B=2 H=16 T=9216 D=128, 23/144 blocks"
 COPY_BYTES = 1 << 30          # profile run: elementwise copy of 1 GiB (reads and writes COPY_BYTES)
 PROFILE_ATTENDS = 40
 GRAPH_CALLS = 20              # C1: calls captured in one HIP graph to time the kernel without host gaps
+SETTLE_CALLS = 200            # untimed calls between the first call and the metric's region
+DENSE_MIN_CALLS = 20          # dense comparator: per-call events over at least this many calls ...
+DENSE_MIN_WARMUP = 10         # ... after at least this many warm-ups
+DENSE_GRAPH_CALLS = 5
 TRAFFIC_FILE = REPO / "profiles" / "attention_c4_traffic.json"
 
 
@@ -111,6 +118,30 @@ def time_gpu(fn, steps: int, warmup: int) -> float:
     end.record()
     torch.cuda.synchronize()
     return start.elapsed_time(end) / steps
+
+
+def time_per_call(fn, calls: int, warmup: int) -> tuple[list[float], list[float]]:
+    """(device ms, host ms) of each of `calls` calls of `fn` after `warmup` untimed ones.
+
+    Device time: a pair of HIP events around each call on the current stream,
+    recorded back to back without host synchronisation (the queue stays full, as
+    in time_gpu); host time: perf_counter around the same enqueue.
+    """
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(calls)]
+    host = []
+    torch.cuda.synchronize()
+    for start, end in events:
+        t0 = time.perf_counter()
+        start.record()
+        fn()
+        end.record()
+        host.append((time.perf_counter() - t0) * 1e3)
+    torch.cuda.synchronize()
+    return [start.elapsed_time(end) for start, end in events], host
 
 
 def time_graph(fn, calls: int, replays: int, warmup: int) -> float:
@@ -505,11 +536,11 @@ def main() -> int:
     if not torch.isfinite(out).all():
         raise RuntimeError("non-finite PISA output")
 
-    # untimed settle: 200 back-to-back calls (~80 ms of GPU work) carry the GPU
-    # through the clock dip that follows the idle first call, so every region
-    # below is timed at settled clocks
+    # untimed settle: SETTLE_CALLS back-to-back calls (~80 ms of GPU work) carry
+    # the GPU through the clock dip that follows the idle first call, so every
+    # region below is timed at settled clocks
     call = lambda: mi355x_pisa.forward_spatial_bhtd(q, k, v, exact_blocks=EXACT)  # noqa: E731
-    for _ in range(200):
+    for _ in range(SETTLE_CALLS):
         call()
     torch.cuda.synchronize()
 
@@ -533,10 +564,15 @@ def main() -> int:
     plan.prepare()
     attend_ms = time_gpu(plan.attend, args.steps, args.warmup)
 
-    # dense exact attention of this library on the same shape (the north star's 1.8x comparator)
-    # and torch's own SDPA on the same views, as context for how strong that comparator is
-    dense_ms = time_gpu(lambda: mi355x_pisa.dense_attention(q, k, v, scale, merged_output=True), args.steps,
-                        max(1, args.warmup // 2))
+    # dense exact attention of this library on the same shape (the north star's 1.8x comparator),
+    # three ways: HIP events around each call (median: one stalled call cannot move it), the host's
+    # enqueue time per call, and DENSE_GRAPH_CALLS calls captured in one HIP graph and replayed;
+    # torch's own SDPA on the same views as context for how strong that comparator is
+    dense = lambda: mi355x_pisa.dense_attention(q, k, v, scale, merged_output=True)  # noqa: E731
+    dense_calls = max(DENSE_MIN_CALLS, args.steps)
+    dense_dev, dense_host = time_per_call(dense, dense_calls, max(DENSE_MIN_WARMUP, args.warmup))
+    dense_ms = statistics.median(dense_dev)
+    dense_graph_ms = time_graph(dense, DENSE_GRAPH_CALLS, 4, 1)
     sdpa_ms = time_gpu(lambda: torch.nn.functional.scaled_dot_product_attention(q, k, v, scale=scale),
                        max(2, args.steps // 4), 2)
 
@@ -598,7 +634,17 @@ def main() -> int:
         "stages_ms": {"prepare": round(prepare_ms, 4), "attend": round(attend_ms, 4)},
         "call_ms_after_1s_idle": round(call_after_idle_ms, 4),
         "first_call_ms": round(first_call_ms, 3),
+        "settle_calls": SETTLE_CALLS,
         "dense_ms": round(dense_ms, 4),
+        "dense_timing": {
+            "method": f"median of HIP events around each of {dense_calls} calls (after "
+                      f"{max(DENSE_MIN_WARMUP, args.warmup)} warm-ups); graph: {DENSE_GRAPH_CALLS} calls "
+                      f"captured in one HIP graph, replayed 4 times",
+            "events_ms_min_max": [round(min(dense_dev), 4), round(max(dense_dev), 4)],
+            "events_ms_mean": round(statistics.fmean(dense_dev), 4),
+            "graph_ms": round(dense_graph_ms, 4),
+            "host_enqueue_ms_median": round(statistics.median(dense_host), 4),
+        },
         "torch_sdpa_dense_ms": round(sdpa_ms, 4),
         "dense_tflops": round(dense_flops / (dense_ms * 1e-3) / 1e12, 2),
         "speedup_vs_dense": round(dense_ms / call_ms, 3),

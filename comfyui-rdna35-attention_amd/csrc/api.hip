@@ -329,6 +329,7 @@ static int prepare_impl(int32_t dtype, int32_t heads, int32_t tokens, int32_t he
                         hipStream_t st) {
     const ForwardBuffers w = carve_forward(workspace, bh, tokens, head_dim, exact_blocks, 2);
     pisa::StatsArgs sa;
+    memset(&sa, 0, sizeof(sa));
     sa.q = to_view(q, heads);
     sa.k = to_view(k, heads);
     sa.v = to_view(v, heads);
@@ -600,8 +601,12 @@ int pisa_hip_block_stats(int32_t dtype, int32_t out_dtype, int32_t batch, int32_
     if (out_dtype != dtype && out_dtype != PISA_DTYPE_F32)
         return fail(PISA_ERR_INVALID_ARGUMENT, "out_dtype must equal dtype or be float32");
     if (batch <= 0 || heads <= 0 || tokens <= 0) return fail(PISA_ERR_INVALID_ARGUMENT, "requires B>0, H>0, T>0");
+    const bool value_sums = (stats_mode & PISA_STATS_FLAG_VALUE_SUMS) != 0;
+    stats_mode &= ~PISA_STATS_FLAG_VALUE_SUMS;
     if (stats_mode != PISA_STATS_MEANS && stats_mode != PISA_STATS_HYD && stats_mode != PISA_STATS_GENERIC)
         return fail(PISA_ERR_INVALID_ARGUMENT, "unknown stats_mode %d", stats_mode);
+    if (value_sums && (stats_mode == PISA_STATS_MEANS || out_dtype != PISA_DTYPE_F32))
+        return fail(PISA_ERR_INVALID_ARGUMENT, "value sums need HYD or GENERIC statistics and float32 outputs");
     // head dims other than 128: the HYD statistics (block_stats_hyd takes any
     // 0 < D <= 256, pisa_kernels.cu:603) and the Triton statistics
     // (pisa_kernel.py:90-130, any width up to 256), here at multiples of 8
@@ -642,6 +647,7 @@ int pisa_hip_block_stats(int32_t dtype, int32_t out_dtype, int32_t batch, int32_
     sa.kc_out = k_centroids;
     sa.vm_out = v_means;
     sa.vm_f32 = out_dtype == PISA_DTYPE_F32;
+    sa.vm_sums = value_sums ? 1 : 0;
     sa.hnorm_out = cov ? h_norm : nullptr;
     sa.hpart = cov ? static_cast<float*>(workspace) : nullptr;
     sa.npad = p.npad;

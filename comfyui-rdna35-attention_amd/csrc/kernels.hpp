@@ -18,6 +18,7 @@ struct StatsArgs {
     float* kc_out;  // [BH][N][D]
     void* vm_out;   // [BH][N][D] (f32 when vm_f32)
     int vm_f32;
+    int vm_sums;    // nonzero: vm_out (f32) receives the per-block value sums instead of the means
     float* hnorm_out;  // [BH][N] (nullable)
     float* hpart;      // [BH][chunks][D][D] (HYD / GENERIC)
     // attention operands (nullable)

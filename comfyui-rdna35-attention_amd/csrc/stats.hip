@@ -187,6 +187,7 @@ __global__ __launch_bounds__(kStatsThreads) __attribute__((amdgpu_waves_per_eu(2
             float mq = ((red[0][0][d] + red[0][1][d]) + red[0][2][d]) + red[0][3][d];
             float mk = ((red[1][0][d] + red[1][1][d]) + red[1][2][d]) + red[1][3][d];
             float mv = ((red[2][0][d] + red[2][1][d]) + red[2][2][d]) + red[2][3][d];
+            const float v_sum = mv;  // the sum itself in HYD / GENERIC mode (pisa_kernel.py:74,78)
             if (MODE == PISA_STATS_HYD) {
                 mq *= inv_len;
                 mk *= inv_len;
@@ -202,7 +203,7 @@ __global__ __launch_bounds__(kStatsThreads) __attribute__((amdgpu_waves_per_eu(2
             if (a.qc_f32) static_cast<float*>(a.qc_out)[o] = mq;
             else static_cast<T*>(a.qc_out)[o] = from_f32<T>(mq);
             a.kc_out[o] = mk;
-            if (a.vm_f32) static_cast<float*>(a.vm_out)[o] = mv;
+            if (a.vm_f32) static_cast<float*>(a.vm_out)[o] = (MODE != PISA_STATS_MEANS && a.vm_sums) ? v_sum : mv;
             else static_cast<T*>(a.vm_out)[o] = from_f32<T>(mv);
             if (a.qc_route) a.qc_route[o] = a.qc_route_round ? to_f32(from_f32<T>(mq)) : mq;
             const int64_t chunk_base = ((int64_t)bh * a.npad + (b & ~63)) * D;  // packed 64-centroid chunk
@@ -385,6 +386,7 @@ __global__ __launch_bounds__(256) void stats_means_kernel(StatsArgs a) {
         mk += red[1][i][d];
         mv += red[2][i][d];
     }
+    const float v_sum = mv;  // pisa_kernel.py:74,78 returns the fp32 sum itself
     const float fl = static_cast<float>(len);
     if (HYD) {
         const float inv_len = 1.0f / fl;
@@ -402,7 +404,7 @@ __global__ __launch_bounds__(256) void stats_means_kernel(StatsArgs a) {
         if (a.qc_f32) static_cast<float*>(a.qc_out)[o] = mq;
         else static_cast<T*>(a.qc_out)[o] = from_f32<T>(mq);
         a.kc_out[o] = mk;
-        if (a.vm_f32) static_cast<float*>(a.vm_out)[o] = mv;
+        if (a.vm_f32) static_cast<float*>(a.vm_out)[o] = a.vm_sums ? v_sum : mv;
         else static_cast<T*>(a.vm_out)[o] = from_f32<T>(mv);
         if (a.qc_route) a.qc_route[o] = mq;
     }

@@ -377,10 +377,10 @@ def _fixed_block_op_fake(q, k, v, scale, causal, mask):
 
 
 # --------------------------------------------------------------------------- statistics
-def _block_stats(q, k, v, mode, out_dtype):
+def _block_stats(q, k, v, mode, out_dtype, value_sums: bool = False):
     """q/k/v: [BH,T,D] (or [B,H,T,D] views).  Returns the 5 HYD outputs (3 for MEANS); h_norm is formed at every
     head dim for HYD statistics and is None for GENERIC statistics off head dim 128 (the Triton statistics form
-    no norms)."""
+    no norms).  value_sums (fp32 outputs): the third output holds the per-block value sums instead of the means."""
     q4 = q if q.ndim == 4 else _as4(q)
     k4 = k if k.ndim == 4 else _as4(k)
     v4 = v if v.ndim == 4 else _as4(v)
@@ -401,7 +401,7 @@ def _block_stats(q, k, v, mode, out_dtype):
         check(
             LIB.pisa_hip_block_stats(
                 dtype_code(q.dtype), dtype_code(out_dtype), batch, heads, tokens, head_dim,
-                view4(q4), view4(k4), view4(v4), grid(), mode,
+                view4(q4), view4(k4), view4(v4), grid(), mode | (_lib.STATS_FLAG_VALUE_SUMS if value_sums else 0),
                 q_centroids.data_ptr(), k_centroids.data_ptr(), v_means.data_ptr(), ptr(h_sum), ptr(h_norm),
                 workspace.data_ptr(), ws_bytes, stream_of(q.device),
             ),

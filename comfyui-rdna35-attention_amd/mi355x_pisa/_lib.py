@@ -23,6 +23,7 @@ DTYPE_F32 = 2
 STATS_MEANS = 0
 STATS_HYD = 1
 STATS_GENERIC = 2
+STATS_FLAG_VALUE_SUMS = 0x100
 ROUTE_HYD = 0
 ROUTE_CENTROID = 1
 NO_SINK = -2

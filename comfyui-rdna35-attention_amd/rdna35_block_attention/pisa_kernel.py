@@ -8,7 +8,7 @@ runs on the library's HIP statistics kernels for gfx950 (the statistics kernel
 at head dim 128, the means and covariance kernels at other widths); H_sum is
 summed in a fixed order, without the reference's float atomics.  Head dims
 must be multiples of 8 here (the reference pads any width up to 256).  The
-value sums are the fp32 block means times the block length.
+value sums are the fp32 sums of each block's rows (pisa_kernel.py:74,78).
 """
 from __future__ import annotations
 
@@ -38,9 +38,8 @@ def pisa_prepare_triton(k: torch.Tensor, v: torch.Tensor, *, block_size: int = 6
         raise ValueError(f"PISA HIP preparation requires D a multiple of 8, got D={head_dim}.")
     native = diagnostics.load_native()
     # the query means are not part of this output: k stands in for q
-    _, k_means, v_means, h_sum, _ = native._block_stats(k, k, v, native._lib.STATS_GENERIC, torch.float32)
+    _, k_means, v_sums, h_sum, _ = native._block_stats(k, k, v, native._lib.STATS_GENERIC, torch.float32,
+                                                       value_sums=True)
     total_blocks = math.ceil(tokens / block_size)
     lengths = [min(block_size, tokens - block * block_size) for block in range(total_blocks)]
-    length_t = torch.tensor(lengths, dtype=torch.float32, device=k.device)
-    v_sums = v_means * length_t[None, :, None]
     return k_means, v_sums, h_sum, lengths

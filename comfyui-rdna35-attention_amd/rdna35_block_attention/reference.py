@@ -94,10 +94,11 @@ def mask_view_bhtt(mask: torch.Tensor, *, batch_heads: int, info: LayoutInfo,
                    device: torch.device) -> torch.Tensor:
     """The whole mask as a [B', H', T, T] broadcast view with B' * H' = BH, row bh = b' * H' + h'.
 
-    Same shape rules and errors as _mask_block (reference.py:114-156); this is
-    the view the HIP fixed-block kernel reads (zero strides for broadcast
-    dims), where the eager loop slices per block.  Masks that are neither
-    bool nor fp32/fp16/bf16 become fp32, the dtype they are added in.
+    The one statement of the mask shape rules (the accepted shapes and errors
+    of reference.py:114-156): the HIP fixed-block kernel reads this view (zero
+    strides for broadcast dims) and the eager path reads its diagonal blocks
+    (_diagonal_blocks, _mask_block).  Masks that are neither bool nor fp32/fp16/bf16 become
+    fp32, the dtype they are added in.
     """
     m = mask.to(device=device)
     if m.dtype != torch.bool and m.dtype not in (torch.float32, torch.float16, torch.bfloat16):
@@ -134,65 +135,68 @@ def mask_view_bhtt(mask: torch.Tensor, *, batch_heads: int, info: LayoutInfo,
 
 def _mask_block(mask: torch.Tensor | None, start: int, end: int, *, batch_heads: int, info: LayoutInfo,
                 device: torch.device) -> torch.Tensor | None:
-    """The [BH, n, n] slice of a 2-D/3-D/4-D attention mask for tokens [start, end)."""
+    """The [BH, n, n] diagonal block of mask_view_bhtt's view for tokens [start, end)."""
     if mask is None:
         return None
-    m = mask.to(device=device)
-    square = (info.tokens, info.tokens)
     n = end - start
-    if m.ndim == 2:
-        if tuple(m.shape[-2:]) != square:
-            raise ValueError(f"2D mask must have shape [T,T], got {tuple(m.shape)}.")
-        return m[start:end, start:end].unsqueeze(0).expand(batch_heads, n, n)
-    if m.ndim == 3:
-        if tuple(m.shape[-2:]) != square:
-            raise ValueError(f"3D mask must end with [T,T], got {tuple(m.shape)}.")
-        part = m[:, start:end, start:end]
-        lead = part.shape[0]
-        if info.batch is not None and lead == info.batch:
-            return part.repeat_interleave(info.heads, dim=0)
-        if lead == 1:
-            return part.expand(batch_heads, n, n)
-        if lead == batch_heads:
-            return part
-        raise ValueError(f"3D mask batch dimension {lead} is not compatible with BH={batch_heads}.")
-    if m.ndim == 4:
-        if info.batch is None or info.heads is None:
-            raise ValueError("4D mask requires a layout with known B and H.")
-        if tuple(m.shape[-2:]) != square:
-            raise ValueError(f"4D mask must end with [T,T], got {tuple(m.shape)}.")
-        if m.shape[0] not in (1, info.batch):
-            raise ValueError(f"4D mask batch dimension {m.shape[0]} is not compatible with B={info.batch}.")
-        if m.shape[1] not in (1, info.heads):
-            raise ValueError(f"4D mask head dimension {m.shape[1]} is not compatible with H={info.heads}.")
-        full = m.expand(info.batch, info.heads, info.tokens, info.tokens)
-        return full[:, :, start:end, start:end].reshape(batch_heads, n, n)
-    raise ValueError(f"Unsupported mask rank {m.ndim}.")
+    view = mask_view_bhtt(mask, batch_heads=batch_heads, info=info, device=device)
+    return view[:, :, start:end, start:end].reshape(batch_heads, n, n)
+
+
+def _diagonal_blocks(view: torch.Tensor, start: int, count: int, size: int) -> torch.Tensor:
+    """[B', H', count, size, size]: the diagonal blocks of a [B', H', T, T] view starting at token `start`.
+
+    One strided view (block j begins size * (query stride + key stride) elements after block j-1);
+    nothing is copied, broadcast dims keep their zero strides.
+    """
+    sub = view[:, :, start:, start:]
+    sb, sh, sq, sk = sub.stride()
+    return sub.as_strided((sub.shape[0], sub.shape[1], count, size, size), (sb, sh, size * (sq + sk), sq, sk),
+                          sub.storage_offset())
+
+
+_SCORE_BUDGET = 1 << 24  # fp32 scores materialised at once by the eager path (64 MiB)
 
 
 def fixed_block_attention_ref(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, block_size: int = 64,
                               scale: float | None = None, causal: bool = False, layout: str = "auto", *,
                               heads: int | None = None, mask: torch.Tensor | None = None) -> torch.Tensor:
-    """Eager fixed block-diagonal attention: every block of `block_size` tokens attends to itself (fp32 math)."""
+    """Eager fixed block-diagonal attention: every block of `block_size` tokens attends to itself.
+
+    fp32 scores, softmax and products, output in the input dtype (reference.py:159-200); the short last
+    block has T mod block_size tokens.  Equal-size blocks run as one batched product over
+    [BH, blocks, size, D] (in groups that keep the scores within _SCORE_BUDGET), with the causal mask and
+    the diagonal blocks of the caller's mask (mask_view_bhtt) applied to the scores.
+    """
     qf, kf, vf, info = normalize_qkv_to_bh_t_d(q, k, v, layout=layout, heads=heads)
     if block_size <= 0:
         raise ValueError("block_size must be positive.")
     bh, tokens, head_dim = qf.shape
     s = float(scale) if scale is not None else 1.0 / math.sqrt(head_dim)
+    view = None if mask is None else mask_view_bhtt(mask, batch_heads=bh, info=info, device=q.device)
     out = torch.empty_like(qf)
-    for start in range(0, tokens, block_size):
-        end = min(start + block_size, tokens)
-        scores = torch.matmul(qf[:, start:end].float(), kf[:, start:end].float().transpose(-2, -1)) * s
-        if causal:
-            upper = torch.ones((end - start, end - start), dtype=torch.bool, device=q.device).triu(1)
-            scores = scores.masked_fill(upper, -torch.inf)
-        block_mask = _mask_block(mask, start, end, batch_heads=bh, info=info, device=q.device)
-        if block_mask is not None:
-            if block_mask.dtype == torch.bool:
-                scores = scores.masked_fill(~block_mask, -torch.inf)
-            else:
-                scores = scores + block_mask.to(scores.dtype)
-        out[:, start:end] = torch.matmul(torch.softmax(scores, dim=-1), vf[:, start:end].float()).to(qf.dtype)
+    full, tail = divmod(tokens, block_size)
+    runs = [(0, full, block_size)] if full else []
+    if tail:
+        runs.append((full * block_size, 1, tail))
+    for first, count, size in runs:
+        group = max(1, _SCORE_BUDGET // (bh * size * size))
+        upper = torch.ones((size, size), dtype=torch.bool, device=q.device).triu(1) if causal else None
+        for j0 in range(0, count, group):
+            n = min(group, count - j0)
+            lo = first + j0 * size
+            hi = lo + n * size
+            qb, kb, vb = (x[:, lo:hi].float().reshape(bh, n, size, head_dim) for x in (qf, kf, vf))
+            scores = torch.matmul(qb, kb.transpose(-2, -1)) * s
+            if upper is not None:
+                scores = scores.masked_fill(upper, -torch.inf)
+            if view is not None:
+                blocks = _diagonal_blocks(view, lo, n, size).reshape(bh, n, size, size)
+                if blocks.dtype == torch.bool:
+                    scores = scores.masked_fill(~blocks, -torch.inf)
+                else:
+                    scores = scores + blocks.to(scores.dtype)
+            out[:, lo:hi] = torch.matmul(torch.softmax(scores, dim=-1), vb).reshape(bh, n * size, head_dim).to(qf.dtype)
     return info.restore(out)
 
 

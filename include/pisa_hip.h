@@ -60,6 +60,10 @@ extern "C" {
 /* generic: centred keys rounded to the input dtype before the product
  * (pisa_kernel.py:49-84, _pisa_block_stats_kernel)                          */
 #define PISA_STATS_GENERIC 2
+/* OR-ed into pisa_hip_block_stats' stats_mode (HYD or GENERIC, out_dtype
+ * PISA_DTYPE_F32): v_means receives the fp32 per-block value sums instead of
+ * the means, the v_sums output of pisa_prepare_triton (pisa_kernel.py:74,78) */
+#define PISA_STATS_FLAG_VALUE_SUMS 0x100
 
 /* ---- routing modes ----------------------------------------------------- */
 /* HYD: r = s * (bf16(qbar) . bf16(kbar)) + ln(h_norm + 1e-5)

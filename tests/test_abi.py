@@ -116,6 +116,15 @@ def test_other_entry_points_validate(lib):
     assert lib.LIB.attn_hip_fixed_block_forward(0, 1, 1, 64, 64, 32, q, k, v, o, 0.1, 0, None) == 2
     assert lib.LIB.pisa_hip_route_topk(1, 2000, 128, None, None, None, 1, 0.1, -2, 3, None, None, None) == 2
     assert lib.LIB.pisa_hip_route_topk(1, 10, 128, None, None, None, 1, 0.1, 5, 3, None, None, None) == 1
+    stats = lambda mode, out_dtype, head_dim=128: lib.LIB.pisa_hip_block_stats(  # noqa: E731
+        0, out_dtype, 1, 1, 64, head_dim, q, k, v, lib.grid(), mode, None, None, None, None, None, None, 0, None)
+    sums = lib.STATS_FLAG_VALUE_SUMS
+    assert stats(lib.STATS_MEANS | sums, 2) == 1        # value sums need HYD / GENERIC statistics ...
+    assert stats(lib.STATS_GENERIC | sums, 0) == 1      # ... and float32 outputs
+    assert stats(lib.STATS_GENERIC | sums, 2) == 1      # accepted flag: fails only for the missing outputs
+    assert b"centroid outputs" in lib.LIB.pisa_hip_last_error()
+    assert stats(lib.STATS_HYD, 0, head_dim=100) == 2   # HYD statistics: multiples of 8 only
+    assert b"multiple of 8" in lib.LIB.pisa_hip_last_error()
     misaligned = lib.PisaView(0x1002, 0, 0, 128)
     assert lib.LIB.pisa_hip_pack_spatial_qkv(0, 1, 1, 9216, 128, misaligned, k, v, lib.grid(1, 96, 96), None,
                                              None, None, None) == 1

@@ -46,8 +46,11 @@ def test_c4_selection_bit_exact_and_oracle_heads(native, anima):
     # the spatial entry point gives the same bits
     spatial = native.forward_spatial_bhtd(q, k, v, exact_blocks=23)
     assert torch.equal(spatial.view(2, 9216, 16, D).permute(0, 2, 1, 3), out)
-    heads = [(0, 0), (1, 15)]
+    # flat heads 0, 9, 18 and 31: with 4 consecutive heads per XCD in the attention kernel's schedule
+    # (4608 query blocks over 8 XCDs), these run on XCDs 0, 2, 4 and 7
+    heads = [(0, 0), (0, 9), (1, 2), (1, 15)]
     for b, h in heads:
+        print(f"C4 oracle head (b={b}, h={h})", flush=True)
         packed = [spatial_to_packed(t[b:b + 1, h:h + 1], 1, 96, 96) for t in (q, k, v)]
         expected, exp_scores, _ = opisa.hyd_forward(*packed, 23, return_selection=True)
         assert_close(np32(scores[b * 16 + h]), exp_scores[0], 1e-4, 1e-4, "C4 routing scores")
