@@ -340,12 +340,17 @@ static int prepare_impl(int32_t dtype, int32_t heads, int32_t tokens, int32_t he
     sa.chunks = p.chunks;
     sa.qc_out = w.qc;
     sa.qc_f32 = 0;
-    sa.kc_out = w.kc;
-    sa.vm_out = w.vm;
+    // bf16 HYD routing at head dim 128 reads the bf16 means and the packed
+    // centroid chunks (route_impl), so the fp32 routing means are not written;
+    // the dtype value means are never read by the forward (the tail reads the
+    // packed value chunks)
+    const bool bf16_route = head_dim == 128 && dtype == PISA_DTYPE_BF16 && route_mode == PISA_ROUTE_HYD;
+    sa.kc_out = bf16_route ? nullptr : w.kc;
+    sa.vm_out = nullptr;
     sa.vm_f32 = 0;
     sa.hnorm_out = w.hnorm;
     sa.hpart = w.hpart;
-    sa.qc_route = w.qc_route;
+    sa.qc_route = bf16_route ? nullptr : w.qc_route;
     // generic routing on HYD statistics multiplies the dtype-rounded q_bar with
     // the fp32 k_bar (generic_pisa.py:120-126,172-173: block_stats_hyd returns
     // q_bar in the input dtype, routed as q_bar.float())
@@ -583,11 +588,17 @@ static int64_t cov_partial_bytes(int bh, int blocks, int padded) {
     return ((int64_t)bh * chunks * padded * padded * 4 + 255) / 256 * 256;
 }
 
+// Padded width of the block statistics off head dim 128: any 0 < D <= 256
+// (dims past D are zero), 0 otherwise.
+static int stats_padded_dim(int head_dim) {
+    return head_dim > 0 && head_dim <= 256 ? pisa::padded_head_dim((head_dim + 7) & ~7) : 0;
+}
+
 int64_t pisa_hip_block_stats_workspace_bytes(int32_t batch, int32_t heads, int32_t tokens, int32_t head_dim) {
     if (batch <= 0 || heads <= 0 || tokens <= 0 || head_dim <= 0) return 0;
     const StatsPlan p = plan_stats(batch * heads, tokens);
     if (head_dim == 128) return (int64_t)batch * heads * p.chunks * head_dim * head_dim * 4;
-    const int padded = pisa::padded_head_dim(head_dim);
+    const int padded = stats_padded_dim(head_dim);
     if (!padded) return 0;
     const int tiles = (padded / 32) * (padded / 32);
     return cov_partial_bytes(batch * heads, p.blocks, padded) + (int64_t)batch * heads * p.blocks * tiles * 4;
@@ -608,12 +619,10 @@ int pisa_hip_block_stats(int32_t dtype, int32_t out_dtype, int32_t batch, int32_
     if (value_sums && (stats_mode == PISA_STATS_MEANS || out_dtype != PISA_DTYPE_F32))
         return fail(PISA_ERR_INVALID_ARGUMENT, "value sums need HYD or GENERIC statistics and float32 outputs");
     // head dims other than 128: the HYD statistics (block_stats_hyd takes any
-    // 0 < D <= 256, pisa_kernels.cu:603) and the Triton statistics
-    // (pisa_kernel.py:90-130, any width up to 256), here at multiples of 8
-    const int padded = head_dim == 128 ? 128 : pisa::padded_head_dim(head_dim);
-    if (head_dim != 128 && !padded)
-        return fail(PISA_ERR_UNSUPPORTED, "block statistics support head_dim a multiple of 8 up to 256, got %d",
-                    head_dim);
+    // 0 < D <= 256, pisa_kernels.cu:605) and the Triton statistics
+    // (pisa_kernel.py:90-130, any width up to 256, padded)
+    const int padded = head_dim == 128 ? 128 : stats_padded_dim(head_dim);
+    if (!padded) return fail(PISA_ERR_UNSUPPORTED, "block statistics support 0 < head_dim <= 256, got %d", head_dim);
     if (!q_centroids || !k_centroids || !v_means) return fail(PISA_ERR_INVALID_ARGUMENT, "centroid outputs are required");
     const bool cov = stats_mode != PISA_STATS_MEANS;
     // h_norm: required for HYD; optional for GENERIC off 128 (the Triton
@@ -621,8 +630,10 @@ int pisa_hip_block_stats(int32_t dtype, int32_t out_dtype, int32_t batch, int32_
     if (cov && (!h_sum || (!h_norm && (stats_mode == PISA_STATS_HYD || head_dim == 128))))
         return fail(PISA_ERR_INVALID_ARGUMENT, "h_sum and h_norm are required");
     int rc;
-    if ((rc = check_grid(grid, tokens)) || (rc = check_view("q", q, 2, true)) || (rc = check_view("k", k, 2, true)) ||
-        (rc = check_view("v", v, 2, true)))
+    // 16-byte row loads at widths that are multiples of 8; element loads otherwise
+    const bool rows16 = head_dim % 8 == 0;
+    if ((rc = check_grid(grid, tokens)) || (rc = check_view("q", q, 2, rows16)) ||
+        (rc = check_view("k", k, 2, rows16)) || (rc = check_view("v", v, 2, rows16)))
         return rc;
     const int bh = batch * heads;
     const StatsPlan p = plan_stats(bh, tokens);

@@ -15,8 +15,8 @@ struct StatsArgs {
     // API outputs
     void* qc_out;   // [BH][N][D] (f32 when qc_f32)
     int qc_f32;
-    float* kc_out;  // [BH][N][D]
-    void* vm_out;   // [BH][N][D] (f32 when vm_f32)
+    float* kc_out;  // [BH][N][D] (nullable at head dim 128)
+    void* vm_out;   // [BH][N][D] (f32 when vm_f32; nullable)
     int vm_f32;
     int vm_sums;    // nonzero: vm_out (f32) receives the per-block value sums instead of the means
     float* hnorm_out;  // [BH][N] (nullable)

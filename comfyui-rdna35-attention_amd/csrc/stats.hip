@@ -202,9 +202,15 @@ __global__ __launch_bounds__(kStatsThreads) __attribute__((amdgpu_waves_per_eu(2
             const int64_t o = ((int64_t)bh * a.blocks + b) * D + d;
             if (a.qc_f32) static_cast<float*>(a.qc_out)[o] = mq;
             else static_cast<T*>(a.qc_out)[o] = from_f32<T>(mq);
-            a.kc_out[o] = mk;
-            if (a.vm_f32) static_cast<float*>(a.vm_out)[o] = (MODE != PISA_STATS_MEANS && a.vm_sums) ? v_sum : mv;
-            else static_cast<T*>(a.vm_out)[o] = from_f32<T>(mv);
+            // (the fused forward routes bf16 HYD on the bf16 means and the packed
+            // centroid chunks, and passes null for the outputs nothing reads)
+            if (a.kc_out) a.kc_out[o] = mk;
+            if (!a.vm_out) {
+            } else if (a.vm_f32) {
+                static_cast<float*>(a.vm_out)[o] = (MODE != PISA_STATS_MEANS && a.vm_sums) ? v_sum : mv;
+            } else {
+                static_cast<T*>(a.vm_out)[o] = from_f32<T>(mv);
+            }
             if (a.qc_route) a.qc_route[o] = a.qc_route_round ? to_f32(from_f32<T>(mq)) : mq;
             const int64_t chunk_base = ((int64_t)bh * a.npad + (b & ~63)) * D;  // packed 64-centroid chunk
             if (a.kbar_pad) static_cast<T*>(a.kbar_pad)[chunk_base + kfrag_elem(b & 63, d, D)] = from_f32<T>(mk);
@@ -321,6 +327,20 @@ __global__ __launch_bounds__(256) void stats_reduce_kernel(ReduceArgs a) {
     if (blockIdx.x == 0) zero_centroid_pad<T>(a, blockIdx.y, threadIdx.x);
 }
 
+// Eight elements d0 .. d0+7 of a row (d0 < head_dim): one 16-byte load when
+// head_dim is a multiple of 8 (rows and pieces 16-byte aligned), else element
+// loads with the dims past head_dim read as zero (rows of an odd width are
+// only element aligned).
+template <typename T, typename vec8>
+__device__ __forceinline__ vec8 load_piece(const char* row, int d0, int head_dim) {
+    if (head_dim % 8 == 0) return load8<vec8>(row + d0 * (int64_t)sizeof(T));
+    vec8 x;
+    const T* r = reinterpret_cast<const T*>(row);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = d0 + e < head_dim ? r[d0 + e] : T(0.0f);
+    return x;
+}
+
 // Block means at head dims other than 128 (H_sum and the H_b norms, when
 // asked for, come from stats_cov_kernel below): one 256-thread workgroup per
 // (batch*head, block).
@@ -351,15 +371,14 @@ __global__ __launch_bounds__(256) void stats_means_kernel(StatsArgs a) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) sq[e] = sk[e] = sv[e] = 0.0f;
     if (mapped && pc * 8 < a.head_dim) {
-        const int64_t off = pc * 8 * (int64_t)sizeof(T);
 #pragma unroll
         for (int pass = 0; pass < kPasses; ++pass) {
             const int r = pass * R + rr;
             if (r < len) {
                 const int raster = base + a.map.intra_offset(r);
-                const vec8 x = load8<vec8>(a.q.data + a.q.row(bh, raster) * sizeof(T) + off);
-                const vec8 y = load8<vec8>(a.k.data + a.k.row(bh, raster) * sizeof(T) + off);
-                const vec8 z = load8<vec8>(a.v.data + a.v.row(bh, raster) * sizeof(T) + off);
+                const vec8 x = load_piece<T, vec8>(a.q.data + a.q.row(bh, raster) * sizeof(T), pc * 8, a.head_dim);
+                const vec8 y = load_piece<T, vec8>(a.k.data + a.k.row(bh, raster) * sizeof(T), pc * 8, a.head_dim);
+                const vec8 z = load_piece<T, vec8>(a.v.data + a.v.row(bh, raster) * sizeof(T), pc * 8, a.head_dim);
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
                     sq[e] += to_f32(x[e]);
@@ -403,9 +422,13 @@ __global__ __launch_bounds__(256) void stats_means_kernel(StatsArgs a) {
         const int64_t o = ((int64_t)bh * a.blocks + b) * a.head_dim + d;
         if (a.qc_f32) static_cast<float*>(a.qc_out)[o] = mq;
         else static_cast<T*>(a.qc_out)[o] = from_f32<T>(mq);
-        a.kc_out[o] = mk;
-        if (a.vm_f32) static_cast<float*>(a.vm_out)[o] = a.vm_sums ? v_sum : mv;
-        else static_cast<T*>(a.vm_out)[o] = from_f32<T>(mv);
+        a.kc_out[o] = mk;  // the covariance kernel centres on these
+        if (!a.vm_out) {
+        } else if (a.vm_f32) {
+            static_cast<float*>(a.vm_out)[o] = a.vm_sums ? v_sum : mv;
+        } else {
+            static_cast<T*>(a.vm_out)[o] = from_f32<T>(mv);
+        }
         if (a.qc_route) a.qc_route[o] = mq;
     }
     if (!a.kbar_pad) return;  // the standalone statistics entry point wants no packed centroids
@@ -490,7 +513,7 @@ __global__ __launch_bounds__(64) void stats_cov_kernel(CovArgs a) {
     const int q4 = lane >> 2;   // tokens 4 q4 .. 4 q4 + 3
     const int dk = 32 * tr + 8 * pc;
     const int dv = 32 * tc + 8 * pc;
-    const bool kdims = dk < a.head_dim;  // head_dim is a multiple of 8
+    const bool kdims = dk < a.head_dim;  // dims past head_dim read as zero (load_piece)
     const bool vdims = dv < a.head_dim;
     const int col = lane & 31;
     const int half = lane >> 5;
@@ -503,13 +526,13 @@ __global__ __launch_bounds__(64) void stats_cov_kernel(CovArgs a) {
         float mean[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e)
-            mean[e] = kdims ? a.kmean[((int64_t)bh * a.blocks + b) * a.head_dim + dk + e] : 0.0f;
+            mean[e] = dk + e < a.head_dim ? a.kmean[((int64_t)bh * a.blocks + b) * a.head_dim + dk + e] : 0.0f;
         vec8 kx[4], vx[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int raster = base + a.map.intra_offset(min(4 * q4 + r, len - 1));
-            if (kdims) kx[r] = load8<vec8>(a.k.data + (a.k.row(bh, raster) + dk) * (int64_t)sizeof(T));
-            if (vdims) vx[r] = load8<vec8>(a.v.data + (a.v.row(bh, raster) + dv) * (int64_t)sizeof(T));
+            if (kdims) kx[r] = load_piece<T, vec8>(a.k.data + a.k.row(bh, raster) * (int64_t)sizeof(T), dk, a.head_dim);
+            if (vdims) vx[r] = load_piece<T, vec8>(a.v.data + a.v.row(bh, raster) * (int64_t)sizeof(T), dv, a.head_dim);
         }
         // the previous block's operand reads by other lanes come before these
         // stores (one wave: the barrier orders its LDS accesses, at no cost)

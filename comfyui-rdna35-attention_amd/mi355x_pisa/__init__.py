@@ -412,18 +412,18 @@ def _block_stats(q, k, v, mode, out_dtype, value_sums: bool = False):
     return q_centroids, k_centroids, v_means, h_sum, h_norm
 
 
-HYD_STATS_HEAD_DIMS = GENERIC_HEAD_DIMS  # block_stats_hyd: 0<D<=256 in the reference, multiples of 8 here
+HYD_STATS_HEAD_DIMS = tuple(range(1, 257))  # block_stats_hyd: any 0<D<=256, as the reference's
 
 
 def block_stats_hyd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor):
     """(q_bar, k_bar fp32, v_bar, H_sum fp32) of [BH,T,D] q/k/v (__init__.py:216-230).
 
-    Any head dim that is a multiple of 8 up to 256 (the reference takes any 0<D<=256), fp16 or bf16.
+    Any head dim 0<D<=256, fp16 or bf16.
     """
     if q.ndim != 3 or q.shape != k.shape or q.shape != v.shape:
         raise ValueError("PISA HIP HYD expects matching [BH,T,D] q/k/v tensors.")
     if q.shape[0] <= 0 or q.shape[1] <= 0 or q.shape[1] > MAX_TOKENS or q.shape[2] not in HYD_STATS_HEAD_DIMS:
-        raise ValueError(f"PISA HIP HYD requires BH>0, 0<T<={MAX_TOKENS}, and 0<D<=256 with D a multiple of 8.")
+        raise ValueError(f"PISA HIP HYD requires BH>0, 0<T<={MAX_TOKENS}, and 0<D<=256.")
     if q.device != k.device or q.device != v.device or not _is_rocm_device(q):
         raise ValueError("PISA HIP HYD requires q/k/v on one PyTorch ROCm device.")
     if q.dtype not in (torch.float16, torch.bfloat16) or k.dtype != q.dtype or v.dtype != q.dtype:
@@ -763,7 +763,7 @@ class _NativeNamespace:
         if k.dtype != q.dtype or v.dtype != q.dtype:
             raise RuntimeError("q, k, and v must have the same dtype.")
         if q.shape[0] <= 0 or q.shape[1] <= 0 or q.shape[2] not in head_dims:
-            dims = f"D={HEAD_DIM}" if tuple(head_dims) == (HEAD_DIM,) else "0<D<=256 with D a multiple of 8"
+            dims = f"D={HEAD_DIM}" if tuple(head_dims) == (HEAD_DIM,) else "0<D<=256"
             raise RuntimeError(f"block statistics require BH>0, T>0, and {dims}.")
         if q.shape[1] > max_tokens:
             raise RuntimeError(f"block statistics support T<={max_tokens}.")
@@ -776,7 +776,7 @@ class _NativeNamespace:
 
     @staticmethod
     def block_stats_hyd(q, k, v):
-        """HYD statistics, all five outputs, at any head dim that is a multiple of 8 up to 256 (pisa_kernels.cu:597-635)."""
+        """HYD statistics, all five outputs, at any head dim 0<D<=256 (pisa_kernels.cu:597-635)."""
         _NativeNamespace._stats_inputs(q, k, v, HYD_STATS_HEAD_DIMS)
         return _block_stats(q, k, v, _lib.STATS_HYD, q.dtype)
 

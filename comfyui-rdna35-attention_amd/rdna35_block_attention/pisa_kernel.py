@@ -6,9 +6,10 @@ H_sum = sum over blocks of dtype(K_b - k_bar_b)^T V_b in fp32 (the centred keys
 rounded to the input dtype, pisa_kernel.py:80-81), and the block lengths.  It
 runs on the library's HIP statistics kernels for gfx950 (the statistics kernel
 at head dim 128, the means and covariance kernels at other widths); H_sum is
-summed in a fixed order, without the reference's float atomics.  Head dims
-must be multiples of 8 here (the reference pads any width up to 256).  The
-value sums are the fp32 sums of each block's rows (pisa_kernel.py:74,78).
+summed in a fixed order, without the reference's float atomics.  Any head
+dim up to 256 is taken, as the reference pads any width (the kernels read
+16-byte pieces at multiples of 8 and single elements otherwise).  The value
+sums are the fp32 sums of each block's rows (pisa_kernel.py:74,78).
 """
 from __future__ import annotations
 
@@ -34,8 +35,6 @@ def pisa_prepare_triton(k: torch.Tensor, v: torch.Tensor, *, block_size: int = 6
     batch_heads, tokens, head_dim = k.shape
     if head_dim > 256:
         raise ValueError(f"PISA Triton preparation requires D<=256, got D={head_dim}.")
-    if head_dim % 8:
-        raise ValueError(f"PISA HIP preparation requires D a multiple of 8, got D={head_dim}.")
     native = diagnostics.load_native()
     # the query means are not part of this output: k stands in for q
     _, k_means, v_sums, h_sum, _ = native._block_stats(k, k, v, native._lib.STATS_GENERIC, torch.float32,

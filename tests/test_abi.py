@@ -123,8 +123,11 @@ def test_other_entry_points_validate(lib):
     assert stats(lib.STATS_GENERIC | sums, 0) == 1      # ... and float32 outputs
     assert stats(lib.STATS_GENERIC | sums, 2) == 1      # accepted flag: fails only for the missing outputs
     assert b"centroid outputs" in lib.LIB.pisa_hip_last_error()
-    assert stats(lib.STATS_HYD, 0, head_dim=100) == 2   # HYD statistics: multiples of 8 only
-    assert b"multiple of 8" in lib.LIB.pisa_hip_last_error()
+    assert stats(lib.STATS_HYD, 0, head_dim=264) == 2   # statistics: any 0 < D <= 256 ...
+    assert b"head_dim <= 256" in lib.LIB.pisa_hip_last_error()
+    assert stats(lib.STATS_HYD, 0, head_dim=0) == 2
+    assert stats(lib.STATS_HYD, 0, head_dim=100) == 1   # ... odd widths accepted: fails only for the outputs
+    assert b"centroid outputs" in lib.LIB.pisa_hip_last_error()
     misaligned = lib.PisaView(0x1002, 0, 0, 128)
     assert lib.LIB.pisa_hip_pack_spatial_qkv(0, 1, 1, 9216, 128, misaligned, k, v, lib.grid(1, 96, 96), None,
                                              None, None, None) == 1
@@ -184,10 +187,10 @@ def test_reference_module_name_keeps_the_reference_contract():
         rdna35_pisa_ck._C.block_stats_hyd(long, long, long)
     with pytest.raises(RuntimeError, match="T<=9216"):
         rdna35_pisa_ck._C.block_stats(long, long, long)
-    # other widths than multiples of 8 are refused with the limit named
-    odd = torch.zeros((1, 64, 100), dtype=torch.bfloat16)
-    with pytest.raises(ValueError, match="multiple of 8"):
-        mi355x_pisa.block_stats_hyd(odd, odd, odd)
+    # widths above 256 are refused with the limit named
+    wide_d = torch.zeros((1, 64, 264), dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="0<D<=256"):
+        mi355x_pisa.block_stats_hyd(wide_d, wide_d, wide_d)
 
 
 @pytest.mark.parametrize("dtype_name, tokens, head_dim", [

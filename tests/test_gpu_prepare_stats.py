@@ -19,6 +19,8 @@ pytestmark = pytest.mark.gpu
     (40, torch.float16, 640),      # padded to 64
     (200, torch.float16, 576),     # padded to 256
     (96, torch.bfloat16, 64),      # a single block
+    (100, torch.bfloat16, 300),    # odd widths: element loads, padded to 128 (the reference pads to 128 too)
+    (37, torch.float16, 130),
 ])
 def test_pisa_prepare_matches_oracle(head_dim, dtype, tokens):
     from rdna35_block_attention.pisa_kernel import pisa_prepare_triton

@@ -3,8 +3,9 @@
 The reference's ``_C.block_stats_hyd`` takes fp16/bf16 [BH,T,D] at any
 0<D<=256 and returns q_bar, k_bar, v_bar, H_sum and ||H_b||_F at every width
 (native/rdna35_pisa_ck/csrc/pisa_kernels.cu:167-244,597-635;
-rdna35_pisa_ck/__init__.py:216-230).  Here every multiple of 8 up to 256 runs
-on the means + covariance kernels; each output is compared with
+rdna35_pisa_ck/__init__.py:216-230).  Here every width off 128 runs on the
+means + covariance kernels (16-byte row pieces at multiples of 8, element
+loads at odd widths); each output is compared with
 ``oracle.pisa.block_stats(..., "hyd")`` (fp32 sums times fp32(1/len), q_bar and
 v_bar rounded to the dtype, keys centred in fp32, float64 products).
 Tolerances: k_bar at fp32 accuracy, q_bar / v_bar within one dtype rounding
@@ -49,7 +50,7 @@ def _check_hyd(outputs, q, k, v, dtype):
 
 @pytest.mark.parametrize("tokens", [65, 576, 9216])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
-@pytest.mark.parametrize("head_dim", [32, 64, 80, 200, 256])
+@pytest.mark.parametrize("head_dim", [32, 64, 80, 200, 256, 1, 37, 100, 255])
 def test_hyd_stats_every_head_dim_match_oracle(native, head_dim, dtype, tokens):
     print(f"[hyd stats] D={head_dim} {dtype} T={tokens}", flush=True)
     bh = 2 if tokens < 9216 else 1
