@@ -110,18 +110,47 @@ def _nonfinite(named) -> list[str]:
     return [name for name, tensor in named if not torch.isfinite(tensor).all().item()]
 
 
+def _partials_nonfinite(q_b, k_b, v_b, idx, k_c, v_m, lengths, scale: float) -> list[str]:
+    """Non-finite partials of one head (debug only): the exact softmax over each query block's selected key
+    blocks and the centroid tail over the others, their outputs and natural-log LSEs, in fp32
+    (generic_pisa.py:188-209 computes the same four tensors with FlexAttention).
+
+    q_b/k_b/v_b: [N, 64, D] block-major (zero rows past T), idx: [N, k] selected blocks, k_c/v_m: [N, D]
+    centroids, lengths: [N] tokens per block.
+    """
+    blocks, _, head_dim = q_b.shape
+    valid = torch.arange(BLOCK_SIZE, device=q_b.device)[None, :] < lengths[:, None]      # [N, 64]
+    qf = q_b.float()
+    k_sel = k_b.float()[idx.long()].reshape(blocks, -1, head_dim)                          # [N, k*64, D]
+    v_sel = v_b.float()[idx.long()].reshape(blocks, -1, head_dim)
+    scores = torch.matmul(qf, k_sel.transpose(1, 2).contiguous()) * scale                 # [N, 64, k*64]
+    scores = scores.masked_fill(~valid[idx.long()].reshape(blocks, 1, -1), -torch.inf)
+    exact_lse = torch.logsumexp(scores, dim=-1)
+    exact_out = torch.matmul(torch.softmax(scores, dim=-1), v_sel)
+    selected = torch.zeros((blocks, blocks), dtype=torch.bool, device=q_b.device)
+    selected.scatter_(1, idx.long(), True)
+    tail = torch.matmul(qf, k_c.float().t().contiguous()) * scale + lengths.float().log()[None, None, :]
+    tail = tail.masked_fill(selected[:, None, :], -torch.inf)
+    approx_lse = torch.logsumexp(tail, dim=-1)
+    approx_out = torch.matmul(torch.softmax(tail, dim=-1), v_m.float())
+    rows = valid[:, :, None]
+    named = (("exact_output", exact_out.masked_fill(~rows, 0.0)), ("exact_lse", exact_lse.masked_fill(~valid, 0.0)),
+             ("approximate_output", approx_out.masked_fill(~rows, 0.0)),
+             ("approximate_lse", approx_lse.masked_fill(~valid, 0.0)))
+    return _nonfinite(named)
+
+
 def _debug_stages(q, k, v, exact_blocks: int, scale: float, grid_sizes) -> None:
     """debug_finite stage checks (generic_pisa.py:174-183,210-219).
 
-    The fused kernel never materialises the exact and approximate partial
-    outputs and LSEs, so the checks cover what exists separately: the block
-    statistics and the routing scores, recomputed here on the same inputs
-    (block-major order of the token grid; head dim 128, where the statistics
-    kernel runs on its own), then the fused output.
+    The block statistics and routing scores are recomputed here on the same
+    inputs (block-major order of the token grid) and checked; then, since the
+    fused kernel never materialises the exact and approximate partial outputs
+    and LSEs, those four are recomputed head by head from the kernel's own
+    selection (_partials_nonfinite) and checked.  The fused output is checked
+    after the call.
     """
     native = diagnostics.load_native()
-    if q.shape[2] != native.HEAD_DIM:  # the statistics kernel runs at head dim 128 only
-        return
     q4, k4, v4 = (t.unsqueeze(1) for t in (q, k, v))
     if grid_sizes is not None:
         q4, k4, v4 = (_pack_video_blocks(t, grid_sizes) for t in (q4, k4, v4))
@@ -130,10 +159,23 @@ def _debug_stages(q, k, v, exact_blocks: int, scale: float, grid_sizes) -> None:
         q_c, k_c, v_m, _, _ = native._block_stats(q4, k4, v4, native._lib.STATS_HYD, q.dtype)
     else:
         q_c, k_c, v_m, _, _ = native._block_stats(q4, k4, v4, native._lib.STATS_GENERIC, torch.float32)
-    scores, _ = native.route_topk(q_c.float(), k_c, None, exact_blocks, scale, round_bf16=False)
+    scores, idx = native.route_topk(q_c.float(), k_c, None, exact_blocks, scale, round_bf16=False)
     failed = _nonfinite((("q_centroids", q_c), ("k_centroids", k_c), ("v_means", v_m), ("route_scores", scores)))
     if failed:
         raise ValueError(f"generic PISA non-finite stages: {','.join(failed)}")
+    bh, tokens, head_dim = q.shape
+    blocks = math.ceil(tokens / BLOCK_SIZE)
+    lengths = torch.full((blocks,), BLOCK_SIZE, device=q.device, dtype=torch.float32)
+    lengths[-1] = tokens - (blocks - 1) * BLOCK_SIZE
+    pad = blocks * BLOCK_SIZE - tokens
+    failed = set()
+    for h in range(bh):
+        q_b, k_b, v_b = (torch.nn.functional.pad(t[h, 0], (0, 0, 0, pad)).reshape(blocks, BLOCK_SIZE, head_dim)
+                         for t in (q4, k4, v4))
+        failed.update(_partials_nonfinite(q_b, k_b, v_b, idx[h], k_c[h].to(q.dtype), v_m[h], lengths, scale))
+    if failed:
+        order = ("exact_output", "exact_lse", "approximate_output", "approximate_lse")
+        raise ValueError(f"generic PISA non-finite stages: {','.join(n for n in order if n in failed)}")
 
 
 def generic_pisa_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, exact_budget: float,

@@ -232,3 +232,22 @@ def test_h3_override_reads_strided_views(tokens):
     expected = oatt.dense_attention(np32(q[:, sel, rows]), np32(k[:, sel]), np32(v[:, sel]))
     got = np32(out).reshape(1, tokens, heads, D)[:, rows][:, :, sel].transpose(0, 2, 1, 3)
     assert_close(got, expected, 5e-2, 5e-2, "h3 heads")
+
+
+@pytest.mark.parametrize("head_dim,grid", [(128, None), (64, (2, 64, 64))])
+def test_generic_debug_finite_checks_every_stage(head_dim, grid):
+    """debug_finite (generic_pisa.py:172-219): finite inputs pass every stage check and give the same bits as
+    the plain call; an infinite key fails the statistics stage."""
+    from rdna35_block_attention.generic_pisa import generic_pisa_attention
+
+    torch.manual_seed(head_dim)
+    tokens = 8192
+    q, k, v = (torch.randn(2, tokens, head_dim, device="cuda", dtype=torch.bfloat16) for _ in range(3))
+    print(f"debug_finite D={head_dim} grid={grid}", flush=True)
+    plain = generic_pisa_attention(q, k, v, exact_budget=0.15, grid_sizes=grid)
+    checked = generic_pisa_attention(q, k, v, exact_budget=0.15, grid_sizes=grid, debug_finite=True)
+    assert torch.equal(plain, checked)
+    k_bad = k.clone()
+    k_bad[1, 100, 3] = float("inf")
+    with pytest.raises(ValueError, match="non-finite stages: .*k_centroids"):
+        generic_pisa_attention(q, k_bad, v, exact_budget=0.15, grid_sizes=grid, debug_finite=True)

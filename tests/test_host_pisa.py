@@ -630,3 +630,32 @@ def test_reference_module_and_probe_names_resolve():
     available, detail = rba.has_triton(import_module=False)
     assert isinstance(available, bool) and isinstance(detail, str)
     assert "has_triton" in rba.__all__
+
+
+def test_debug_partials_name_the_nonfinite_stage():
+    """debug_finite's partial-stage check (generic_pisa.py:210-219): a NaN in a selected key block's values
+    reaches only the exact partial, a NaN centroid value only the approximate one; rows past T are ignored."""
+    gen = torch.Generator().manual_seed(4)
+    blocks, d = 4, 16
+    q_b, k_b, v_b = (torch.randn((blocks, 64, d), generator=gen) for _ in range(3))
+    lengths = torch.tensor([64.0, 64.0, 64.0, 10.0])
+    for t in (q_b, k_b, v_b):
+        t[3, 10:] = 0.0                                  # zero rows past T, as the caller pads
+    idx = torch.tensor([[0], [1], [1], [3]], dtype=torch.int32)
+    k_c, v_m = k_b.sum(1) / lengths[:, None], v_b.sum(1) / lengths[:, None]
+    check = generic_pisa._partials_nonfinite
+    assert check(q_b, k_b, v_b, idx, k_c, v_m, lengths, 0.25) == []
+    q_pad = q_b.clone()
+    q_pad[3, 20:] = float("nan")                         # rows past T never count
+    assert check(q_pad, k_b, v_b, idx, k_c, v_m, lengths, 0.25) == []
+    v_bad = v_b.clone()
+    v_bad[1, 5, 2] = float("nan")                        # block 1 is selected by query blocks 1 and 2
+    assert check(q_b, k_b, v_bad, idx, k_c, v_m, lengths, 0.25) == ["exact_output"]
+    v_m_bad = v_m.clone()
+    v_m_bad[2, 0] = float("nan")                         # centroid 2 is unselected for every query block
+    assert check(q_b, k_b, v_b, idx, k_c, v_m_bad, lengths, 0.25) == ["approximate_output"]
+    k_bad = k_b.clone()
+    k_bad[0, 0, 0] = float("inf")
+    q_pos = q_b.abs() + 0.1                              # +inf score -> NaN softmax row, inf LSE
+    failed = check(q_pos, k_bad, v_b, idx, k_c, v_m, lengths, 0.25)
+    assert "exact_lse" in failed and "exact_output" in failed
