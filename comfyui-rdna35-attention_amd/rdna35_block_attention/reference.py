@@ -46,48 +46,57 @@ def _canonical_layout(layout: str) -> str:
     return _LAYOUT_ALIASES[key]
 
 
+# Rank and shape wording of each canonical layout (the accepted layouts and their errors
+# are the reference's interface, reference.py:38-111).
+_LAYOUT_RANK = {"bhtd": 4, "bh_t_d": 3, "bthd": 3}
+_LAYOUT_SHAPE = {"bhtd": "[B,H,T,D]", "bh_t_d": "[BH,T,D]", "bthd": "[B,T,H*D]"}
+
+
+def _bhtd_view(x: torch.Tensor, layout: str, heads: int | None) -> torch.Tensor:
+    """x in `layout` as a [B, H, T, D] tensor (a view where the strides allow; flat [BH,T,D] is B = 1)."""
+    if layout == "bhtd":
+        return x
+    if layout == "bh_t_d":
+        return x.unsqueeze(0)
+    b, t, channels = x.shape
+    return x.reshape(b, t, heads, channels // heads).permute(0, 2, 1, 3)
+
+
 def normalize_qkv_to_bh_t_d(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, layout: str = "auto",
                             heads: int | None = None):
-    """Flatten q/k/v to contiguous [B*H, T, D]; returns (q, k, v, LayoutInfo with restore())."""
+    """Flatten q/k/v to contiguous [B*H, T, D]; returns (q, k, v, LayoutInfo with restore()).
+
+    Every layout is first seen as [B, H, T, D] (_bhtd_view); restore() maps a [B*H, T, D] result back to
+    the caller's layout and shape.  LayoutInfo reports B and H where the layout defines them.
+    """
     if q.shape != k.shape or q.shape != v.shape:
         raise ValueError(
             f"Fixed block self-attention requires q/k/v to have identical shapes, got {q.shape}, {k.shape}, {v.shape}.")
     chosen = _canonical_layout(layout)
     if chosen == "auto":
-        if q.ndim not in (3, 4):
+        chosen = {4: "bhtd", 3: "bh_t_d"}.get(q.ndim, "")
+        if not chosen:
             raise ValueError(f"Cannot infer layout for rank-{q.ndim} tensor.")
-        chosen = "bhtd" if q.ndim == 4 else "bh_t_d"
-
-    if chosen == "bhtd":
-        if q.ndim != 4:
-            raise ValueError(f"layout='bhtd' expects [B,H,T,D], got rank {q.ndim}.")
-        b, h, t, d = q.shape
-        flat = [x.contiguous().reshape(b * h, t, d) for x in (q, k, v)]
-        return (*flat, LayoutInfo(chosen, b, h, t, d, lambda out: out.reshape(b, h, t, d)))
-
-    if chosen == "bh_t_d":
-        if q.ndim != 3:
-            raise ValueError(f"layout='bh_t_d' expects [BH,T,D], got rank {q.ndim}.")
-        bh, t, d = q.shape
-        return (q.contiguous(), k.contiguous(), v.contiguous(),
-                LayoutInfo(chosen, None, None, t, d, lambda out: out.reshape(bh, t, d)))
-
-    if q.ndim != 3:
-        raise ValueError(f"layout='bthd' expects [B,T,H*D], got rank {q.ndim}.")
-    if heads is None or heads <= 0:
-        raise ValueError("layout='bthd' requires a positive heads argument.")
-    b, t, channels = q.shape
-    if channels % heads:
-        raise ValueError(f"channels={channels} is not divisible by heads={heads}.")
-    d = channels // heads
-
-    def to_flat(x: torch.Tensor) -> torch.Tensor:
-        return x.reshape(b, t, heads, d).transpose(1, 2).contiguous().reshape(b * heads, t, d)
+    if q.ndim != _LAYOUT_RANK[chosen]:
+        raise ValueError(f"layout='{chosen}' expects {_LAYOUT_SHAPE[chosen]}, got rank {q.ndim}.")
+    if chosen == "bthd":
+        if heads is None or heads <= 0:
+            raise ValueError("layout='bthd' requires a positive heads argument.")
+        if q.shape[-1] % heads:
+            raise ValueError(f"channels={q.shape[-1]} is not divisible by heads={heads}.")
+    views = [_bhtd_view(x, chosen, heads) for x in (q, k, v)]
+    b, h, t, d = views[0].shape
+    flat = [x.reshape(b * h, t, d).contiguous() for x in views]
+    caller_shape = q.shape
 
     def restore(out: torch.Tensor) -> torch.Tensor:
-        return out.reshape(b, heads, t, d).transpose(1, 2).contiguous().reshape(b, t, channels)
+        out4 = out.reshape(b, h, t, d)
+        if chosen == "bthd":
+            out4 = out4.permute(0, 2, 1, 3)
+        return out4.contiguous().reshape(caller_shape)
 
-    return (to_flat(q), to_flat(k), to_flat(v), LayoutInfo(chosen, b, heads, t, d, restore))
+    known = chosen != "bh_t_d"
+    return (*flat, LayoutInfo(chosen, b if known else None, h if known else None, t, d, restore))
 
 
 def mask_view_bhtt(mask: torch.Tensor, *, batch_heads: int, info: LayoutInfo,
