@@ -25,7 +25,10 @@ Also measured in the same process, in this order:
   * the dense exact attention kernel of this library on the same shape (the
     1.8x comparator of the north star: median of per-call HIP events, with the
     graph-replay time and host enqueue time beside it) and torch's SDPA on the
-    same views;
+    same views; speedup_vs_dense = the dense call's median per-call time over
+    the PISA call's metric time (HIP events on both sides; replayed from a HIP
+    graph, the PISA call measured 7-20 % slower than issued eagerly, so graph
+    times are reported for the dense call only);
   * the metric's region again right after one idle second
     (call_ms_after_1s_idle);
   * the CPU baseline: the fp32 torch port of the HYD forward
@@ -647,6 +650,7 @@ def main() -> int:
         },
         "torch_sdpa_dense_ms": round(sdpa_ms, 4),
         "dense_tflops": round(dense_flops / (dense_ms * 1e-3) / 1e12, 2),
+        # HIP events on both sides (the dense call's median over single calls: one stalled call cannot move it)
         "speedup_vs_dense": round(dense_ms / call_ms, 3),
         "baseline_ms_gfx1151": BASELINE_MS,
     }
