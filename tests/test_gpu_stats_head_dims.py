@@ -101,3 +101,23 @@ def test_reference_stats_choice_on_device_matches_generic_stats_mode(native, dty
     dtype = getattr(torch, dtype_name_)
     x = torch.zeros((1, tokens, 128), dtype=dtype, device="cuda")
     assert _reference_stats_choice(rdna35_pisa_ck, x, x, x) == native.generic_stats_mode(tokens, 128, dtype)
+
+
+def test_reference_name_traces_under_torch_compile(native):
+    """torch.compile(fullgraph=True) through rdna35_pisa_ck (the reference compiles its ops the same way,
+    test_forward.py:203-209): HYD statistics at head dim 64 and the HYD forward give the eager bits."""
+    import rdna35_pisa_ck
+
+    q, k, v = _inputs(2, 300, 64, torch.bfloat16, seed=5)
+
+    def stats(q, k, v):
+        return rdna35_pisa_ck.block_stats_hyd(q, k, v)
+
+    for a, b in zip(torch.compile(stats, backend="inductor", fullgraph=True)(q, k, v), stats(q, k, v)):
+        assert torch.equal(a, b)
+    q2, k2, v2 = _inputs(2, 256, 128, torch.bfloat16, seed=6)
+
+    def forward(q, k, v):
+        return rdna35_pisa_ck.forward(q, k, v, exact_blocks=1)
+
+    assert torch.equal(torch.compile(forward, backend="inductor", fullgraph=True)(q2, k2, v2), forward(q2, k2, v2))
