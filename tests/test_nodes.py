@@ -171,3 +171,49 @@ def test_fixed_block_benchmark_runs_reference_on_cpu(nodes):
         1, 2, 128, 32, "float16", "auto", False)
     assert "dispatch backend: reference" in text
     assert "max abs error vs reference: 0" in text
+
+
+WIDGET_TYPES = ("BOOLEAN", "INT", "FLOAT", "STRING")
+
+
+def _widget_ok(spec, value) -> bool:
+    kind = spec[0]
+    opts = spec[1] if len(spec) > 1 else {}
+    if isinstance(kind, list):
+        return value in kind
+    if kind == "BOOLEAN":
+        return isinstance(value, bool)
+    if kind == "INT":
+        return isinstance(value, int) and opts.get("min", value) <= value <= opts.get("max", value)
+    if kind == "FLOAT":
+        return isinstance(value, (int, float)) and opts.get("min", value) <= value <= opts.get("max", value)
+    return isinstance(value, str)
+
+
+def test_reference_workflows_load_on_these_nodes(nodes):
+    """The attention nodes of the reference's saved workflows (tests/golden/reference_workflow_nodes.json, written
+    from /root/reference/workflows by tests/golden/make_workflow_nodes.py) bind to these node classes: same node
+    id, the saved widget values valid for the widgets in declaration order, the same socket names, and the patch
+    accepts the values."""
+    import json
+    import pathlib
+
+    fixture = json.loads((pathlib.Path(__file__).parent / "golden" / "reference_workflow_nodes.json").read_text())
+    assert sum(len(rows) for rows in fixture.values()) == 3
+    for workflow, rows in fixture.items():
+        for row in rows:
+            cls = nodes.NODE_CLASS_MAPPINGS[row["type"]]
+            spec = cls.INPUT_TYPES()
+            ordered = list(spec["required"].items()) + list(spec.get("optional", {}).items())
+            widgets = [(name, s) for name, s in ordered if isinstance(s[0], list) or s[0] in WIDGET_TYPES]
+            sockets = [name for name, s in ordered if not (isinstance(s[0], list) or s[0] in WIDGET_TYPES)]
+            values = row["widgets_values"]
+            assert len(values) <= len(widgets), (workflow, row["type"])
+            for (name, s), value in zip(widgets, values):
+                assert _widget_ok(s, value), (workflow, row["type"], name, value)
+            assert row["inputs"] == sockets, (workflow, row["type"])
+            assert list(cls.RETURN_NAMES) == row["outputs"], (workflow, row["type"])
+            model = FakeModelPatcher()
+            kwargs = {name: value for (name, _), value in zip(widgets, values)}
+            out, info = getattr(cls(), cls.FUNCTION)(model, **kwargs)
+            assert isinstance(info, str) and out is not None
