@@ -6,8 +6,8 @@
 //     the grid map, so raster spatial/video layouts need no packing pass),
 //   * reduces the column sums (lane shuffles + one LDS exchange) into the
 //     block means q_bar, k_bar, v_bar,
-//   * centres the keys in fp32, splits them into a bf16 pair hi + lo and
-//     stages hi, lo and V transposed in LDS,
+//   * centres the keys in fp32, splits them into a pair hi + lo of the input
+//     dtype (kSplitScale) and stages hi, lo and V transposed in LDS,
 //   * computes H_b = (K - k_bar)^T V with 32x32x16 MFMAs (hi and lo passes,
 //     fp32 accumulation), its Frobenius norm, and accumulates H_b into a
 //     per-workgroup partial of H_sum held in the MFMA accumulators,
@@ -28,6 +28,15 @@
 namespace pisa {
 
 constexpr int kStatsThreads = 256;
+
+// The HYD statistics centre the keys in fp32 and carry each centred value c as
+// a pair hi + lo of the input dtype for the MFMA.  |c| <= 2 * max|k| exceeds
+// fp16's range for keys near it, so fp16 pairs carry c / 2 and the fp32 products
+// are doubled after the MFMA; scaling by a power of two is exact, so the
+// results equal those of the unscaled pair wherever it does not overflow
+// (bf16 has fp32's range and no scale).
+template <typename T> struct SplitScale { static constexpr float value = 1.0f; };
+template <> struct SplitScale<f16_t> { static constexpr float value = 0.5f; };
 constexpr int kLdsRow = kBlock + 8;  // padded LDS row (elements) of a transposed block
 constexpr int kKRow = 128 + 8;       // padded LDS row (elements) of a raw key row
 
@@ -234,8 +243,9 @@ __global__ __launch_bounds__(kStatsThreads) __attribute__((amdgpu_waves_per_eu(2
             for (int r = 0; r < 4; ++r) {
                 const bool valid = rq * 4 + r < len;
                 const float c = valid ? to_f32(kv[r][e]) - km : 0.0f;
-                hi[r] = from_f32<T>(c);
-                lo[r] = (MODE == PISA_STATS_HYD) ? from_f32<T>(c - to_f32(hi[r])) : T(0.0f);
+                const float cs = MODE == PISA_STATS_HYD ? c * SplitScale<T>::value : c;
+                hi[r] = from_f32<T>(cs);
+                lo[r] = (MODE == PISA_STATS_HYD) ? from_f32<T>(cs - to_f32(hi[r])) : T(0.0f);
                 vt[r] = vv[r][e];
             }
             typedef T vec4 __attribute__((ext_vector_type(4)));
@@ -274,6 +284,9 @@ __global__ __launch_bounds__(kStatsThreads) __attribute__((amdgpu_waves_per_eu(2
                 hb = mfma32(ah[ks], bv, hb);
                 if (MODE == PISA_STATS_HYD) hb = mfma32(al[ks], bv, hb);
             }
+            if (MODE == PISA_STATS_HYD && SplitScale<T>::value != 1.0f)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) hb[v] *= 1.0f / SplitScale<T>::value;
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
                 ss += hb[v] * hb[v];
@@ -483,8 +496,8 @@ int launch_stats_means(int dtype, int padded, const StatsArgs& a, int bh_count, 
 //   HYD = false: the Triton statistics every head dim up to 256 takes
 //     (pisa_kernel.py:71-84): centred keys rounded to the input dtype.
 //   HYD = true: block_stats_hyd_kernel (pisa_kernels.cu:214-243): keys
-//     centred in fp32, carried as a dtype pair hi + lo (hi = dtype(c),
-//     lo = dtype(c - hi)) with one MFMA pass each.
+//     centred in fp32, carried as a dtype pair hi + lo (hi = dtype(c s),
+//     lo = dtype(c s - hi), s = SplitScale) with one MFMA pass each.
 // When normpart is set, the wave also writes the tile's sum of squares of
 // H_b for every block ([BH][N][tiles]); cov_reduce_kernel adds the tiles in
 // order into ||H_b||_F.  Rows past a short last block contribute zero, as
@@ -543,7 +556,8 @@ __global__ __launch_bounds__(64) void stats_cov_kernel(CovArgs a) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const bool valid = 4 * q4 + r < len;
-                const float c = (valid && kdims) ? to_f32(kx[r][e]) - mean[e] : 0.0f;
+                const float c0 = (valid && kdims) ? to_f32(kx[r][e]) - mean[e] : 0.0f;
+                const float c = HYD ? c0 * SplitScale<T>::value : c0;
                 ck[r] = from_f32<T>(c);
                 if (HYD) cl[r] = from_f32<T>(c - to_f32(ck[r]));
                 cv[r] = (valid && vdims) ? vx[r][e] : T(0.0f);
@@ -567,6 +581,9 @@ __global__ __launch_bounds__(64) void stats_cov_kernel(CovArgs a) {
                 hb = mfma32(kl, vb, hb);
             }
         }
+        if (HYD && SplitScale<T>::value != 1.0f)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) hb[v] *= 1.0f / SplitScale<T>::value;
         float ss = 0.0f;
 #pragma unroll
         for (int v = 0; v < 16; ++v) {

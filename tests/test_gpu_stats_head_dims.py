@@ -121,3 +121,19 @@ def test_reference_name_traces_under_torch_compile(native):
         return rdna35_pisa_ck.forward(q, k, v, exact_blocks=1)
 
     assert torch.equal(torch.compile(forward, backend="inductor", fullgraph=True)(q2, k2, v2), forward(q2, k2, v2))
+
+
+@pytest.mark.parametrize("head_dim", [128, 64, 37])
+def test_fp16_keys_near_the_range_limit_centre_without_overflow(native, head_dim):
+    """Keys of -60000 with one +60000 row per block centre to about 1.18e5, past fp16's 65504: the reference
+    centres in fp32 (pisa_kernels.cu:225-227) and its H_b stays finite, and so must the fp16 statistics here
+    (head dim 128: stats_kernel; others: stats_cov_kernel)."""
+    print(f"[hyd stats fp16 near max] D={head_dim}", flush=True)
+    gen = torch.Generator().manual_seed(head_dim)
+    k = torch.full((2, 300, head_dim), -60000.0)
+    k[:, ::64] = 60000.0
+    q, v = (torch.randn((2, 300, head_dim), generator=gen) for _ in range(2))
+    q, k, v = (t.to(torch.float16).cuda() for t in (q, k, v))
+    qc, kc, vm, hs, hn = native._C.block_stats_hyd(q, k, v)
+    assert torch.isfinite(hs).all() and torch.isfinite(hn).all()
+    _check_hyd((qc, kc, vm, hs, hn), q, k, v, torch.float16)
