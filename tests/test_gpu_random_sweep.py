@@ -11,7 +11,8 @@ statistics), a dtype, a head dim, a token count or a frames x height x width gri
   restatement of __init__.py:233-316 and generic_pisa.py:141-232) on the kernel's selection, so a near-tie
   between two blocks cannot move a row (bf16 atol = rtol = 5e-2, fp16 2e-2).
 
-The cases are listed in the test ids; every run draws the same ones.
+The exact attention and fixed block-diagonal kernels get sweeps of their own (below).  The cases are listed in
+the test ids; every run draws the same ones.
 """
 from __future__ import annotations
 
@@ -22,6 +23,7 @@ import pytest
 import torch
 
 from helpers import assert_close, np32
+from oracle import attention as oatt
 from oracle import layout as olayout
 from oracle import numerics as onum
 from oracle import pisa as opisa
@@ -105,3 +107,100 @@ def test_random_case_matches_oracle(native, case):
     raster = np.empty_like(ref)
     raster[:, order] = ref
     assert_close(np32(out[0]), raster, TOL[dtype], TOL[dtype], _case_id(case))
+
+
+def _dense_cases(count=60, seed=77):
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(count):
+        dtype = [torch.bfloat16, torch.float16][i % 2]
+        head_dim = int(rng.choice([8, 40, 64, 80, 96, 128, 160, 200, 256]))
+        q_tokens = int(rng.choice([1, 63, 64, int(rng.integers(2, 700))]))
+        kv_tokens = int(rng.choice([1, 64, 65, int(rng.integers(2, 700))]))
+        layout = ["bhtd", "bthd"][int(rng.integers(0, 2))]
+        cases.append((dtype, head_dim, q_tokens, kv_tokens, int(rng.integers(1, 3)), int(rng.integers(1, 5)),
+                      layout, bool(rng.random() < 0.3), int(rng.integers(1 << 30))))
+    return cases
+
+
+def _dense_id(c):
+    dtype, d, tq, tk, b, h, layout, merged, _ = c
+    return f"{'bf16' if dtype == torch.bfloat16 else 'f16'}-D{d}-Tq{tq}-Tk{tk}-B{b}H{h}-{layout}{'-merged' if merged else ''}"
+
+
+@pytest.mark.parametrize("case", _dense_cases(), ids=_dense_id)
+def test_random_dense_case_matches_oracle(native, case):
+    """Exact attention (triton_kernel.py:113-197 semantics) on seeded random shapes: ragged and single-token query
+    and key counts, head dims 8-256, contiguous [B,H,T,D] or raster [B,T,H,D] storage, merged [B,T,H*D] output."""
+    dtype, head_dim, q_tokens, kv_tokens, batch, heads, layout, merged, seed = case
+    print(f"[sweep dense] {_dense_id(case)}", flush=True)
+    gen = torch.Generator().manual_seed(seed)
+
+    def make(tokens):
+        if layout == "bhtd":
+            return torch.randn((batch, heads, tokens, head_dim), generator=gen).to(dtype).cuda()
+        return torch.randn((batch, tokens, heads, head_dim), generator=gen).to(dtype).cuda().permute(0, 2, 1, 3)
+
+    q, k, v = make(q_tokens), make(kv_tokens), make(kv_tokens)
+    s = head_dim ** -0.5
+    out = native.dense_attention(q, k, v, s, merged_output=merged)
+    ref = oatt.dense_attention(np32(q), np32(k), np32(v), s)
+    got = np32(out.view(batch, q_tokens, heads, head_dim).permute(0, 2, 1, 3)) if merged else np32(out)
+    assert_close(got, ref, TOL[dtype], TOL[dtype], _dense_id(case))
+
+
+FIXED_TOL = {torch.float32: 1e-5, torch.float16: 2e-2, torch.bfloat16: 5e-2}  # masked: fp32 probabilities
+FIXED_TOL_TRITON = {torch.float16: 2e-3, torch.bfloat16: 1e-2}                # unmasked 16-bit: probabilities in dtype
+
+
+def _fixed_cases(count=60, seed=91):
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(count):
+        dtype = [torch.float32, torch.bfloat16, torch.float16][i % 3]
+        mask = ["none", "none", "bool", "f32", "f16", "bf16"][int(rng.integers(0, 6))]
+        broadcast = ["full", "batch", "head", "shared"][int(rng.integers(0, 4))]
+        cases.append((dtype, int(rng.choice([32, 64, 128])), int(rng.choice([1, 64, 65, int(rng.integers(2, 600))])),
+                      int(rng.integers(1, 3)), int(rng.integers(1, 4)), bool(rng.random() < 0.5), mask, broadcast,
+                      int(rng.integers(1 << 30))))
+    return cases
+
+
+def _fixed_id(c):
+    dtype, d, t, b, h, causal, mask, bc, _ = c
+    name = {torch.float32: "f32", torch.bfloat16: "bf16", torch.float16: "f16"}[dtype]
+    return f"{name}-D{d}-T{t}-B{b}H{h}-c{int(causal)}-{mask}{'-' + bc if mask != 'none' else ''}"
+
+
+@pytest.mark.parametrize("case", _fixed_cases(), ids=_fixed_id)
+def test_random_fixed_block_case_matches_oracle(native, case):
+    """Fixed 64-token block-diagonal attention (reference.py:159-200; triton_kernel.py:53-100 for unmasked 16-bit
+    calls, whose probabilities are rounded to the dtype) on seeded random shapes: ragged last blocks, T = 1, causal,
+    bool and additive masks broadcast over batch, heads or both through zero strides."""
+    dtype, head_dim, tokens, batch, heads, causal, mask_kind, broadcast, seed = case
+    print(f"[sweep fixed] {_fixed_id(case)}", flush=True)
+    gen = torch.Generator().manual_seed(seed)
+    q, k, v = (torch.randn((batch, heads, tokens, head_dim), generator=gen).to(dtype).cuda() for _ in range(3))
+    s = head_dim ** -0.5
+    view = None
+    if mask_kind != "none":
+        shape = {"full": (batch, heads), "batch": (batch, 1), "head": (1, heads), "shared": (1, 1)}[broadcast]
+        raw = torch.rand((*shape, tokens, tokens), generator=gen)
+        keep_own = torch.eye(tokens, dtype=torch.bool)  # every row keeps its own key
+        if mask_kind == "bool":
+            m = (raw < 0.7) | keep_own
+        else:
+            m = torch.where(raw < 0.2, torch.tensor(float("-inf")), raw * 3.0 - 1.5)
+            m = torch.where(keep_own, raw * 0.1, m).to({"f32": torch.float32, "f16": torch.float16,
+                                                       "bf16": torch.bfloat16}[mask_kind])
+        view = m.cuda().expand(batch, heads, tokens, tokens)
+    out = native.fixed_block_attention(q, k, v, s, causal, view)
+    if view is None:
+        prob = None if dtype == torch.float32 else ("bf16" if dtype == torch.bfloat16 else "f16")
+        expected = oatt.fixed_block_attention(np32(q), np32(k), np32(v), 64, s, causal, prob_dtype=prob)
+        tol = FIXED_TOL[dtype] if dtype == torch.float32 else FIXED_TOL_TRITON[dtype]
+    else:
+        host = view.cpu().numpy() if mask_kind == "bool" else np32(view)
+        expected = oatt.fixed_block_attention(np32(q), np32(k), np32(v), 64, s, causal, mask=host)
+        tol = FIXED_TOL[dtype]
+    assert_close(np32(out), expected, tol, tol, _fixed_id(case))
