@@ -324,7 +324,7 @@ def run_workload(name: str, args) -> dict:
         kernel_ms = time_graph(call, GRAPH_CALLS, max(1, args.steps // GRAPH_CALLS), 2)
         nbytes = 4 * math.prod(shape) * 4
         achieved = nbytes / (kernel_ms * 1e-3)
-        roof = {"bound": "hbm", "kernel": "fixed_block_f32_mfma_kernel", "achieved": round(achieved / 1e9, 1),
+        roof = {"bound": "hbm", "kernel": "fixed_block_f32x3_kernel", "achieved": round(achieved / 1e9, 1),
                 "peak": PEAK_HBM_BYTES / 1e9, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_BYTES, 4),
                 "traffic": None, "timed": f"{GRAPH_CALLS} calls per HIP graph replay"}
         # the HBM floor at this size: one device copy that reads and writes the same 33.5 MB

@@ -1,8 +1,10 @@
 // Fixed block-diagonal attention: every 64-token block attends only to itself.
 //
-// Three kernels.  bf16/fp16 calls without a mask run fixed_block_mfma_kernel
+// Four kernels.  bf16/fp16 calls without a mask run fixed_block_mfma_kernel
 // (matrix cores, the reference's Triton semantics, below); fp32 calls without
-// a mask run fixed_block_f32_mfma_kernel (fp32 matrix cores, below).  Masked
+// a mask run fixed_block_f32x3_kernel (head dims 32, 64: fp32 products from
+// exact three-part bf16 splits on the bf16 matrix cores) or
+// fixed_block_f32_mfma_kernel (head dim 128: fp32 matrix cores).  Masked
 // calls and rows that are not 16-byte aligned - the calls the reference sends
 // to its eager fp32 loop - run fixed_block_kernel:
 //
@@ -468,6 +470,203 @@ __global__ __launch_bounds__(256) void fixed_block_f32_mfma_kernel(View q, View 
     }
 }
 
+// fp32 fixed-block attention on the bf16 matrix cores (head dims 32 and 64;
+// at 128 its LDS tables would leave one workgroup per CU, and
+// fixed_block_f32_mfma_kernel above measured faster).  Every fp32 operand x
+// is split exactly into three bf16 parts by truncation, x = hi + mid + lo
+// (hi = x with the low 16 bits cleared, mid likewise of x - hi, lo = the rest,
+// which has at most 8 significant bits), and a product a.b is formed from the
+// six terms whose weight is at least 2^-16 of a_hi.b_hi (mm, hl, lh, hm, mh,
+// hh, smallest first), accumulated in fp32 by v_mfma_f32_16x16x32_bf16: six
+// products at sixteen times the fp32 matrix rate.  The dropped terms (ml, lm,
+// ll) weigh at most 2^-24 of a_hi.b_hi, about one fp32 rounding.
+// Wave w owns queries 16w .. 16w+15 (lane column c = lane % 16, lane group
+// g = lane / 16), as in fixed_block_f32_mfma_kernel:
+//   S^T = K Q^T: k-step s contracts dims 32s + 8g .. +7 in lane group g; the
+//     key parts are staged in LDS row-major, the query parts split in
+//     registers; accumulator r of key tile n is key 16n + 4g + r.
+//   O^T = V^T P^T: k-step j contracts keys 32j .. 32j+31, lane group g taking
+//     keys 32j + 4g + (0..3) and 32j + 16 + 4g + (0..3) - exactly the
+//     probabilities the lane holds in key tiles 2j and 2j + 1 - so the value
+//     parts are staged transposed with the keys of each 32-key step in that
+//     order (slot of key kk: 8 (kk/4 % 4) + 4 (kk/16) + kk % 4).
+template <int D>
+__global__ __launch_bounds__(256) void fixed_block_f32x3_kernel(View q, View k, View v, OutView o, int tokens,
+                                                                int nblocks, float scale, int causal) {
+    typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+    constexpr int KS = D / 32;      // 32-dim k-steps of the score products
+    constexpr int MT = D / 16;      // 16-dim output tiles
+    constexpr int kKRow = D + 8;    // LDS row of a key part (bf16)
+    constexpr int kVRow = 64 + 8;   // LDS row of a transposed value part (bf16)
+    constexpr int DG = D / 4;       // 4-dim groups of a row
+    constexpr int TILES = 16 * DG;  // 4 keys x 4 dims staging tiles of the block
+    __shared__ __attribute__((aligned(16))) __bf16 kp[3][64 * kKRow];
+    __shared__ __attribute__((aligned(16))) __bf16 vp[3][D * kVRow];
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int w = t >> 6;
+    const int c = lane & 15;
+    const int g = lane >> 4;
+    const int bh = blockIdx.x / nblocks;
+    const int start = (blockIdx.x - bh * nblocks) * 64;
+    const int len = min(64, tokens - start);
+    auto at = [&](const View& x, int r) {
+        return reinterpret_cast<const float*>(x.data) + x.row(bh, start + min(r, len - 1));
+    };
+    // exact three-way split by truncation
+    auto split = [](float x, float& h, float& m, float& l) {
+        h = __uint_as_float(__float_as_uint(x) & 0xffff0000u);
+        const float r = x - h;
+        m = __uint_as_float(__float_as_uint(r) & 0xffff0000u);
+        l = r - m;
+    };
+    auto bf = [](float x) { return __builtin_bit_cast(__bf16, (unsigned short)(__float_as_uint(x) >> 16)); };
+
+    // ---- staging: thread t stages 4 keys x 4 dims tiles (key group kg, dim group dg)
+    for (int tile = t; tile < TILES; tile += 256) {
+        const int kg = tile / DG;
+        const int dg = tile - kg * DG;
+        f32x4 xk[4], xv[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            xk[r] = *reinterpret_cast<const f32x4*>(at(k, 4 * kg + r) + 4 * dg);
+            xv[r] = *reinterpret_cast<const f32x4*>(at(v, 4 * kg + r) + 4 * dg);
+        }
+        // key parts row-major: 4 dims of each of the 4 keys
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            __bf16 ph[4], pm[4], pl[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float h, m, l;
+                split(xk[r][e], h, m, l);
+                ph[e] = bf(h); pm[e] = bf(m); pl[e] = bf(l);
+            }
+            const int off = (4 * kg + r) * kKRow + 4 * dg;
+            typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+            *reinterpret_cast<bf16x4*>(&kp[0][off]) = bf16x4{ph[0], ph[1], ph[2], ph[3]};
+            *reinterpret_cast<bf16x4*>(&kp[1][off]) = bf16x4{pm[0], pm[1], pm[2], pm[3]};
+            *reinterpret_cast<bf16x4*>(&kp[2][off]) = bf16x4{pl[0], pl[1], pl[2], pl[3]};
+        }
+        // value parts transposed: 4 keys of each of the 4 dims, at the slots of
+        // keys 4kg .. 4kg+3 (consecutive)
+        const int kk = (4 * kg) & 31;
+        const int slot = ((4 * kg) & ~31) + 8 * ((kk >> 2) & 3) + 4 * (kk >> 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            __bf16 ph[4], pm[4], pl[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float h, m, l;
+                split(xv[r][e], h, m, l);
+                ph[r] = bf(h); pm[r] = bf(m); pl[r] = bf(l);
+            }
+            const int off = (4 * dg + e) * kVRow + slot;
+            typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+            *reinterpret_cast<bf16x4*>(&vp[0][off]) = bf16x4{ph[0], ph[1], ph[2], ph[3]};
+            *reinterpret_cast<bf16x4*>(&vp[1][off]) = bf16x4{pm[0], pm[1], pm[2], pm[3]};
+            *reinterpret_cast<bf16x4*>(&vp[2][off]) = bf16x4{pl[0], pl[1], pl[2], pl[3]};
+        }
+    }
+    // ---- query parts: lane (c, g) holds dims 32s + 8g .. +7 of query 16w + c
+    bf16x8 qh[KS], qm[KS], ql[KS];
+    {
+        const float* qr = at(q, 16 * w + c);
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+            const f32x4 a = *reinterpret_cast<const f32x4*>(qr + 32 * s + 8 * g);
+            const f32x4 b = *reinterpret_cast<const f32x4*>(qr + 32 * s + 8 * g + 4);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                float h, m, l;
+                split(e < 4 ? a[e] : b[e - 4], h, m, l);
+                qh[s][e] = bf(h); qm[s][e] = bf(m); ql[s][e] = bf(l);
+            }
+        }
+    }
+    __syncthreads();
+
+    auto kfrag = [&](int part, int n, int s) {
+        return *reinterpret_cast<const bf16x8*>(&kp[part][(16 * n + c) * kKRow + 32 * s + 8 * g]);
+    };
+    f32x4 sacc[4];
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+        sacc[n] = f32x4(0.0f);
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+            const bf16x8 kh = kfrag(0, n, s), km = kfrag(1, n, s), kl = kfrag(2, n, s);
+            sacc[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(km, qm[s], sacc[n], 0, 0, 0);
+            sacc[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, ql[s], sacc[n], 0, 0, 0);
+            sacc[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kl, qh[s], sacc[n], 0, 0, 0);
+            sacc[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, qm[s], sacc[n], 0, 0, 0);
+            sacc[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(km, qh[s], sacc[n], 0, 0, 0);
+            sacc[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, qh[s], sacc[n], 0, 0, 0);
+        }
+    }
+
+    // softmax of query column 16w + c (as fixed_block_f32_mfma_kernel)
+    const int query = 16 * w + c;
+    float mx = -__builtin_inff();
+#pragma unroll
+    for (int n = 0; n < 4; ++n)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int key = 16 * n + 4 * g + r;
+            const bool dead = key >= len || (causal && key > query);
+            sacc[n][r] = dead ? -__builtin_inff() : sacc[n][r] * scale;
+            mx = fmaxf(mx, sacc[n][r]);
+        }
+    {
+        const float2 p16 = pair_xor16(mx);
+        mx = max_xor32(fmaxf(p16.x, p16.y));
+    }
+    const float m_use = (mx == -__builtin_inff()) ? 0.0f : mx;
+    float sum = 0.0f;
+#pragma unroll
+    for (int n = 0; n < 4; ++n)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            sacc[n][r] = expf(sacc[n][r] - m_use);
+            sum += sacc[n][r];
+        }
+    sum = add_xor32(add_xor16(sum));
+    const float inv = sum > 0.0f ? 1.0f / sum : __builtin_nanf("");
+    // probability parts: k-step j takes key tiles 2j (slots 0-3) and 2j+1 (slots 4-7)
+    bf16x8 ph[2], pm[2], pl[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            float h, m, l;
+            split(sacc[2 * j + (e >> 2)][e & 3] * inv, h, m, l);
+            ph[j][e] = bf(h); pm[j][e] = bf(m); pl[j][e] = bf(l);
+        }
+    auto vfrag = [&](int part, int mt, int j) {
+        return *reinterpret_cast<const bf16x8*>(&vp[part][(16 * mt + c) * kVRow + 32 * j + 8 * g]);
+    };
+    f32x4 oacc[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        oacc[mt] = f32x4(0.0f);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const bf16x8 vh = vfrag(0, mt, j), vm = vfrag(1, mt, j), vl = vfrag(2, mt, j);
+            oacc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vm, pm[j], oacc[mt], 0, 0, 0);
+            oacc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, pl[j], oacc[mt], 0, 0, 0);
+            oacc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vl, ph[j], oacc[mt], 0, 0, 0);
+            oacc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, pm[j], oacc[mt], 0, 0, 0);
+            oacc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vm, ph[j], oacc[mt], 0, 0, 0);
+            oacc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, ph[j], oacc[mt], 0, 0, 0);
+        }
+    }
+    if (query >= len) return;
+    // accumulator r of output tile mt is dim 16mt + 4g + r of query 16w + c
+    float* dst = reinterpret_cast<float*>(o.data) + o.row(bh, start + query);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) *reinterpret_cast<f32x4*>(dst + 16 * mt + 4 * g) = oacc[mt];
+}
+
 template <typename T, int D>
 static void launch_fixed_mfma(const View& q, const View& k, const View& v, const OutView& o, int tokens, int nblocks,
                               int bh_count, float scale, int causal, hipStream_t stream) {
@@ -478,8 +677,12 @@ static void launch_fixed_mfma(const View& q, const View& k, const View& v, const
 template <int D>
 static void launch_fixed_f32_mfma(const View& q, const View& k, const View& v, const OutView& o, int tokens,
                                   int nblocks, int bh_count, float scale, int causal, hipStream_t stream) {
-    hipLaunchKernelGGL((fixed_block_f32_mfma_kernel<D>), dim3(bh_count * nblocks), dim3(256), 0, stream, q, k, v, o,
-                       tokens, nblocks, scale, causal);
+    if constexpr (D <= 64)
+        hipLaunchKernelGGL((fixed_block_f32x3_kernel<D>), dim3(bh_count * nblocks), dim3(256), 0, stream, q, k, v, o,
+                           tokens, nblocks, scale, causal);
+    else
+        hipLaunchKernelGGL((fixed_block_f32_mfma_kernel<D>), dim3(bh_count * nblocks), dim3(256), 0, stream, q, k, v,
+                           o, tokens, nblocks, scale, causal);
 }
 
 template <typename T>
@@ -501,7 +704,7 @@ int launch_fixed_t(int head_dim, const View& q, const View& k, const View& v, co
             if (head_dim == 32) launch_fixed_f32_mfma<32>(q, k, v, o, tokens, nblocks, bh_count, scale, causal, stream);
             else if (head_dim == 64) launch_fixed_f32_mfma<64>(q, k, v, o, tokens, nblocks, bh_count, scale, causal, stream);
             else launch_fixed_f32_mfma<128>(q, k, v, o, tokens, nblocks, bh_count, scale, causal, stream);
-            return pisa_host::check_launch("fixed_block_f32_mfma_kernel");
+            return pisa_host::check_launch("fixed_block_f32 kernel");
         }
     } else {
         if (mask.kind == PISA_MASK_NONE && rows16) {  // the reference's Triton path: no mask (dispatch.py:50-79)
