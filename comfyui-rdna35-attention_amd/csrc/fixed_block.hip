@@ -470,6 +470,18 @@ __global__ __launch_bounds__(256) void fixed_block_f32_mfma_kernel(View q, View 
     }
 }
 
+// e^x for x <= 0 in fp32: 2^(x log2 e) on v_exp_f32, with the rounding error of
+// the product (an fma) and the low part of log2 e carried into a first-order
+// factor (its neglected square is below 1e-10 for x >= -100); -inf gives 0.
+// Four full-rate instructions and one exponential where expf's range handling
+// takes about a dozen (C1 9.43 -> 9.06 us, same error against float64).
+__device__ __forceinline__ float exp_nonpos(float x) {
+    const float hi = x * kLog2e;
+    const float lo = fmaf(x, kLog2e, -hi) + x * 1.925963e-8f;  // log2(e) - fp32(log2(e)) = 1.925963e-8
+    const float e = __builtin_amdgcn_exp2f(hi) * fmaf(lo, 0.69314718f, 1.0f);
+    return x == -__builtin_inff() ? 0.0f : e;
+}
+
 // fp32 fixed-block attention on the bf16 matrix cores (head dims 32 and 64;
 // at 128 its LDS tables would leave one workgroup per CU, and
 // fixed_block_f32_mfma_kernel above measured faster).  Every fp32 operand x
@@ -627,7 +639,7 @@ __global__ __launch_bounds__(256) void fixed_block_f32x3_kernel(View q, View k, 
     for (int n = 0; n < 4; ++n)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            sacc[n][r] = expf(sacc[n][r] - m_use);
+            sacc[n][r] = exp_nonpos(sacc[n][r] - m_use);
             sum += sacc[n][r];
         }
     sum = add_xor32(add_xor16(sum));
