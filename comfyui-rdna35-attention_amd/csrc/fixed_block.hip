@@ -485,9 +485,10 @@ __device__ __forceinline__ float exp_nonpos(float x) {
 // fp32 fixed-block attention on the bf16 matrix cores (head dims 32 and 64;
 // at 128 its LDS tables would leave one workgroup per CU, and
 // fixed_block_f32_mfma_kernel above measured faster).  Every fp32 operand x
-// is split exactly into three bf16 parts by truncation, x = hi + mid + lo
-// (hi = x with the low 16 bits cleared, mid likewise of x - hi, lo = the rest,
-// which has at most 8 significant bits), and a product a.b is formed from the
+// is split into three bf16 parts by truncation, x = hi + mid + lo (hi = x with
+// the low 16 bits cleared, mid likewise of x - hi, lo = the rest, which has at
+// most 8 significant bits: exact for |x| >= 2^-110, below which lo is an fp32
+// denormal and its bf16 part loses at most 2^-133), and a product a.b is formed from the
 // six terms whose weight is at least 2^-16 of a_hi.b_hi (mm, hl, lh, hm, mh,
 // hh, smallest first), accumulated in fp32 by v_mfma_f32_16x16x32_bf16: six
 // products at sixteen times the fp32 matrix rate.  The dropped terms (ml, lm,
