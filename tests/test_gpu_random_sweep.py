@@ -12,11 +12,13 @@ statistics), a dtype, a head dim, a token count or a frames x height x width gri
   between two blocks cannot move a row (bf16 atol = rtol = 5e-2, fp16 2e-2).
 
 The exact attention and fixed block-diagonal kernels get sweeps of their own (below).  The cases are listed in
-the test ids; every run draws the same ones.
+the test ids; every run draws the same ones.  MI355X_SWEEP_SCALE (an integer, default 1) multiplies the number of
+cases and MI355X_SWEEP_SEED (default 0) offsets the seeds, for longer runs over other cases.
 """
 from __future__ import annotations
 
 import math
+import os
 
 import numpy as np
 import pytest
@@ -30,9 +32,11 @@ from oracle import pisa as opisa
 
 pytestmark = pytest.mark.gpu
 TOL = {torch.bfloat16: 5e-2, torch.float16: 2e-2}
+SCALE = int(os.environ.get("MI355X_SWEEP_SCALE", "1"))
+SEED = int(os.environ.get("MI355X_SWEEP_SEED", "0"))
 
 
-def _cases(count=120, seed=2026):
+def _cases(count=120 * SCALE, seed=2026 + SEED):
     rng = np.random.default_rng(seed)
     grids = [(1, 16, 24), (2, 16, 16), (1, 32, 32), (3, 8, 24), (1, 8, 8)]
     cases = []
@@ -109,7 +113,7 @@ def test_random_case_matches_oracle(native, case):
     assert_close(np32(out[0]), raster, TOL[dtype], TOL[dtype], _case_id(case))
 
 
-def _dense_cases(count=60, seed=77):
+def _dense_cases(count=60 * SCALE, seed=77 + SEED):
     rng = np.random.default_rng(seed)
     cases = []
     for i in range(count):
@@ -153,7 +157,7 @@ FIXED_TOL = {torch.float32: 1e-5, torch.float16: 2e-2, torch.bfloat16: 5e-2}  # 
 FIXED_TOL_TRITON = {torch.float16: 2e-3, torch.bfloat16: 1e-2}                # unmasked 16-bit: probabilities in dtype
 
 
-def _fixed_cases(count=60, seed=91):
+def _fixed_cases(count=60 * SCALE, seed=91 + SEED):
     rng = np.random.default_rng(seed)
     cases = []
     for i in range(count):
