@@ -220,7 +220,7 @@ def test_max_size_video_pisa_matches_oracle(native):
 
 @pytest.mark.parametrize("grid", [(2, 64, 64), (1, 64, 128), (8, 32, 32)])
 def test_wan_ltx_t8192_generic_routes_on_hyd_statistics(native, grid):
-    """Generic PISA at T = 8192, D = 128, bf16 (the Wan/LTX regime of README.md:110-112): the
+    """Generic PISA at T = 8192, D = 128, bf16 (the Wan/LTX regime of the reference's README.md:110-112): the
     reference routes on the native HYD statistics there (generic_pisa.py:120-126).  Selection
     against the oracle's for every head, output against the oracle on two heads."""
     from mi355x_pisa.synthetic import video_qkv
