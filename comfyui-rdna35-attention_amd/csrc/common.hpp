@@ -71,6 +71,12 @@ template <typename V> __device__ __forceinline__ V load8(const void* p) {
     u32x4 raw = *reinterpret_cast<const u32x4*>(p);
     return __builtin_bit_cast(V, raw);
 }
+// The same load with the non-temporal hint, for rows a kernel reads once and
+// no later launch reads again: they then do not displace from the L2 and the
+// last-level cache the data that later launches do re-read.
+template <typename V> __device__ __forceinline__ V load8_nt(const void* p) {
+    return __builtin_bit_cast(V, __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p)));
+}
 template <typename V> __device__ __forceinline__ void store8(void* p, V v) {
     *reinterpret_cast<u32x4*>(p) = __builtin_bit_cast(u32x4, v);
 }

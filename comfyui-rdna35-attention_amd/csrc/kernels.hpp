@@ -55,7 +55,8 @@ struct ReduceArgs {
 // added in chunk order (the sum does not depend on how the loads are
 // batched), H_sum is written in fp32 and its transpose as packed dtype
 // fragments (both optional).  `tile_lds` is a 32 x 33 float array; the call
-// ends with a barrier, so it can be called again on the same array.
+// ends with a barrier, so it can be called again on the same array.  The
+// partials are read once, with the non-temporal hint (C4 prepare -0.7 us).
 template <typename T, int D = 128>
 __device__ inline void reduce_h_tile(const ReduceArgs& a, int bh, int tile, float (*tile_lds)[33], int t) {
     const int tr = tile / (D / 32);  // 32-row tile index
@@ -72,7 +73,7 @@ __device__ inline void reduce_h_tile(const ReduceArgs& a, int bh, int tile, floa
         for (int u = 0; u < kBatch; ++u)
 #pragma unroll
             for (int it = 0; it < 4; ++it)
-                x[u][it] = src[(int64_t)min(ch0 + u, a.chunks - 1) * D * D + off[it]];  // unconditional
+                x[u][it] = __builtin_nontemporal_load(&src[(int64_t)min(ch0 + u, a.chunks - 1) * D * D + off[it]]);  // unconditional
 #pragma unroll
         for (int u = 0; u < kBatch; ++u)
 #pragma unroll
