@@ -54,8 +54,11 @@ def _float32(value: float) -> float:
     return converted
 
 
+_HIP = torch.version.hip is not None  # a ROCm build of PyTorch (its "cuda" devices are HIP devices)
+
+
 def _is_rocm_device(tensor: torch.Tensor) -> bool:
-    return tensor.device.type == "cuda" and torch.version.hip is not None
+    return tensor.device.type == "cuda" and _HIP
 
 
 def _validate_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
@@ -101,24 +104,29 @@ def _check_inputs(what: str, q, k, v, *, dtypes, same_tokens: bool) -> None:
 
     k and v must match each other; q must share their batch, heads and head
     dim, and their token count unless `same_tokens` is False (cross attention).
+    Every attribute is read once: this runs on every eager call, whose host time
+    bounds small calls (C1's kernel runs 9 us).
     """
-    if not all(isinstance(tensor, torch.Tensor) for tensor in (q, k, v)):
+    if not (isinstance(q, torch.Tensor) and isinstance(k, torch.Tensor) and isinstance(v, torch.Tensor)):
         raise TypeError(f"{what}: q, k, and v must be torch tensors.")
-    if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
-        raise ValueError(f"{what}: expects [B,H,T,D] q/k/v, got {q.ndim}-D/{k.ndim}-D/{v.ndim}-D")
-    if k.shape != v.shape:
-        raise ValueError(f"{what}: k {tuple(k.shape)} and v {tuple(v.shape)} must match")
-    if q.shape[0] != k.shape[0] or q.shape[1] != k.shape[1] or q.shape[3] != k.shape[3]:
-        raise ValueError(f"{what}: q {tuple(q.shape)} and k/v {tuple(k.shape)} must share batch, heads and head dim")
-    if same_tokens and q.shape[2] != k.shape[2]:
-        raise ValueError(f"{what}: q and k/v must have the same token count, got {q.shape[2]} and {k.shape[2]}")
-    if min(q.shape) <= 0 or min(k.shape) <= 0:
+    qs, ks, vs = q.shape, k.shape, v.shape
+    if len(qs) != 4 or len(ks) != 4 or len(vs) != 4:
+        raise ValueError(f"{what}: expects [B,H,T,D] q/k/v, got {len(qs)}-D/{len(ks)}-D/{len(vs)}-D")
+    if ks != vs:
+        raise ValueError(f"{what}: k {tuple(ks)} and v {tuple(vs)} must match")
+    if qs[0] != ks[0] or qs[1] != ks[1] or qs[3] != ks[3]:
+        raise ValueError(f"{what}: q {tuple(qs)} and k/v {tuple(ks)} must share batch, heads and head dim")
+    if same_tokens and qs[2] != ks[2]:
+        raise ValueError(f"{what}: q and k/v must have the same token count, got {qs[2]} and {ks[2]}")
+    if min(qs) <= 0 or min(ks) <= 0:
         raise ValueError(f"{what}: every dimension must be positive")
-    if q.device != k.device or q.device != v.device or not _is_rocm_device(q):
+    device = q.device
+    if device != k.device or device != v.device or device.type != "cuda" or not _HIP:
         raise ValueError(f"{what}: q/k/v must be on one PyTorch ROCm device.")
-    if q.dtype not in dtypes or k.dtype != q.dtype or v.dtype != q.dtype:
+    dtype = q.dtype
+    if dtype not in dtypes or k.dtype != dtype or v.dtype != dtype:
         names = "/".join(str(d).replace("torch.", "") for d in dtypes)
-        raise ValueError(f"{what}: q/k/v must share one dtype of {names}, got {q.dtype}/{k.dtype}/{v.dtype}")
+        raise ValueError(f"{what}: q/k/v must share one dtype of {names}, got {dtype}/{k.dtype}/{v.dtype}")
     if q.stride(3) != 1 or k.stride(3) != 1 or v.stride(3) != 1:
         raise ValueError(f"{what}: head_dim must have unit stride")
 
