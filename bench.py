@@ -29,6 +29,10 @@ Also measured in the same process, in this order:
     the PISA call's metric time (HIP events on both sides; replayed from a HIP
     graph, the PISA call measured 7-20 % slower than issued eagerly, so graph
     times are reported for the dense call only);
+  * torch.matmul of two random bf16 [8192, 8192] matrices (hipBLASLt) as
+    library_gemm: the rate a vendor-tuned matrix-core kernel sustains on the
+    same box, whose clocks drop under matrix-core load with random operands,
+    beside the published peak the roofline uses;
   * the metric's region again right after one idle second
     (call_ms_after_1s_idle);
   * the CPU baseline: the fp32 torch port of the HYD forward
@@ -87,6 +91,9 @@ SETTLE_CALLS = 200            # untimed calls between the first call and the met
 DENSE_MIN_CALLS = 20          # dense comparator: per-call events over at least this many calls ...
 DENSE_MIN_WARMUP = 10         # ... after at least this many warm-ups
 DENSE_GRAPH_CALLS = 5
+GEMM_N = 8192                 # library GEMM comparator: 1.1 TFLOP per call
+GEMM_CALLS = 30
+GEMM_WARMUP = 10
 TRAFFIC_FILE = REPO / "profiles" / "attention_c4_traffic.json"
 
 
@@ -593,6 +600,13 @@ def main() -> int:
     dense_graph_ms = time_graph(dense, DENSE_GRAPH_CALLS, 4, 1)
     sdpa_ms = time_gpu(lambda: torch.nn.functional.scaled_dot_product_attention(q, k, v, scale=scale),
                        max(2, args.steps // 4), 2)
+    # the vendor library's bf16 GEMM on the same box (torch.matmul -> hipBLASLt, random operands): what a tuned
+    # matrix-core kernel sustains at the clocks the power limit leaves under that load, beside the published peak
+    gemm_a = torch.randn((GEMM_N, GEMM_N), device=device, dtype=torch.bfloat16)
+    gemm_b = torch.randn((GEMM_N, GEMM_N), device=device, dtype=torch.bfloat16)
+    gemm_ms = time_gpu(lambda: torch.matmul(gemm_a, gemm_b), GEMM_CALLS, GEMM_WARMUP)
+    gemm_tflops = 2.0 * GEMM_N ** 3 / (gemm_ms * 1e-3) / 1e12
+    del gemm_a, gemm_b
 
     # the plan's stages reproduce the call bit for bit; then the metric's region
     # again right after an idle second (after 1 s idle the attention kernel runs
@@ -664,6 +678,14 @@ def main() -> int:
             "host_enqueue_ms_median": round(statistics.median(dense_host), 4),
         },
         "torch_sdpa_dense_ms": round(sdpa_ms, 4),
+        "library_gemm": {
+            "kernel": f"torch.matmul bf16 [{GEMM_N},{GEMM_N}] x [{GEMM_N},{GEMM_N}] (hipBLASLt), random operands",
+            "ms": round(gemm_ms, 4),
+            "achieved": round(gemm_tflops, 1),
+            "unit": "TFLOP/s",
+            "frac_of_peak": round(gemm_tflops * 1e12 / PEAK_BF16_FLOPS, 4),
+            "attention_kernel_vs_gemm": round(achieved / (gemm_tflops * 1e12), 4),
+        },
         "dense_tflops": round(dense_flops / (dense_ms * 1e-3) / 1e12, 2),
         # HIP events on both sides (the dense call's median over single calls: one stalled call cannot move it)
         "speedup_vs_dense": round(dense_ms / call_ms, 3),

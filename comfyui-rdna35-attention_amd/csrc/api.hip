@@ -460,6 +460,7 @@ static int attend_impl(int32_t dtype, int32_t heads, int32_t tokens, int32_t hea
     aa.q_blocks = p.blocks;
     aa.kv_blocks = p.blocks;
     aa.scale_log2 = scale * pisa::kLog2e;
+    aa.inv_scale_log2 = 1.0f / aa.scale_log2;
     aa.idx = w.idx;
     aa.exact = exact_blocks;
     aa.kbar = static_cast<const char*>(w.kbar_pad);
@@ -855,6 +856,7 @@ int attn_hip_dense_forward(int32_t dtype, int32_t batch, int32_t heads, int32_t 
     aa.q_blocks = (q_tokens + pisa::kBlock - 1) / pisa::kBlock;
     aa.kv_blocks = kv_blocks;
     aa.scale_log2 = scale * pisa::kLog2e;
+    aa.inv_scale_log2 = 1.0f / aa.scale_log2;
     aa.head_dim = head_dim;
     return pisa::launch_attention(dtype, padded, false, false, aa, bh, st);
 }

@@ -31,6 +31,8 @@
 // Reference semantics: exact tile __init__.py:127-137,286-298; tail
 // __init__.py:139-164 (score_mod: selected -> -inf, else + ln(len)); dense
 // online softmax triton_kernel.py:113-160.
+#include <type_traits>
+
 #include "kernels.hpp"
 
 namespace pisa {
@@ -408,7 +410,22 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
 #pragma unroll
             for (int ss = 0; ss < 2; ++ss) vf[md][2 * mt + ss] = ld_frag(p, md * 4 + 2 * mt + ss);
     };
-    auto scores_half = [&](const vec8 (&k)[KT], f32x16 (&s)[NT]) {
+    // Centroid chunks of bf16 problems get their score bias from the matrix
+    // core: one more MFMA per query tile adds A x B with A's first two
+    // contraction slots holding the key's bias / c as a bf16 hi + lo pair
+    // (bias_frag: 16 significant bits, relative error below 2^-16) and B's
+    // holding ones, so the softmax of a centroid half is the exact blocks' one
+    // (scores times c in the exponent's fma).  fp16 keeps the VALU transform
+    // (transform_tail): bias / c can exceed fp16's range at small softmax
+    // scales.
+    constexpr bool kBiasMfma = TAIL && std::is_same<T, bf16_t>::value;
+    const vec8 ones_frag = [&] {
+        vec8 x;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = T((half == 0 && e < 2) ? 1.0f : 0.0f);
+        return x;
+    }();
+    auto scores_half = [&](const vec8 (&k)[KT], f32x16 (&s)[NT], const vec8* bias = nullptr) {
         uint32_t qoff = lane * 16;
         if constexpr (QLDS) asm volatile("" : "+v"(qoff));
 #pragma unroll
@@ -419,6 +436,9 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
         for (int t = 0; t < KT; ++t)
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt) s[nt] = mfma32(k[t], qfrag(nt, t, qoff), s[nt]);
+        if (kBiasMfma && bias)
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) s[nt] = mfma32(*bias, ones_frag, s[nt]);
     };
     auto pv_half = [&](int mt, const vec8 (&pf)[NT][2]) {
 #pragma unroll
@@ -431,6 +451,25 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
     // Whether half chunks of chunk x (table row `row`) need transform_half: tail
     // chunks and a short last key block (wave-uniform).
     auto special = [&](int x, int row) { return is_tail(x) || (row + 1) * kBlock > a.kv_tokens; };
+    // A operand of the bias MFMA of half mt of chunk x (table row `row`):
+    // lane (0, col) holds the bias of centroid 64 row + 32 mt + col divided by
+    // c, as bf16 hi and lo; every other slot is zero (all of them for an exact
+    // chunk).  Selected blocks and padding get -inf (hi), others log2(len).
+    auto bias_frag = [&](int x, int row, int mt) -> vec8 {
+        vec8 f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) f[e] = T(0.0f);
+        if (!is_tail(x) || half != 0) return f;
+        const int base = row * kBlock + mt * 32;
+        const uint32_t word = (2 * row + mt < a.mask_words) ? my_mask[2 * row + mt] : 0u;
+        const int j = base + col;
+        const bool dead = ((word >> col) & 1u) != 0u || j >= a.centroids;
+        const float b = (j == a.centroids - 1 ? a.last_len_log2 : 6.0f) * a.inv_scale_log2;
+        const T hi = from_f32<T>(b);
+        f[0] = dead ? T(-__builtin_inff()) : hi;
+        f[1] = dead ? T(0.0f) : from_f32<T>(b - to_f32(hi));
+        return f;
+    };
     // Tail bias of half mt of the centroid chunk in table row `row`; the
     // scores come out in log2 units (returns the factor 1).
     auto transform_tail = [&](int row, int mt, f32x16 (&s)[NT]) -> float {
@@ -477,6 +516,7 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
             }
             return c;
         }
+        if constexpr (kBiasMfma) return c;
         return transform_tail(row, mt, s);
     };
 
@@ -492,7 +532,9 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
     auto check_half = [&](int x, int row, int mt, f32x16 (&s)[NT], bool enable, int kind) -> float {
         float mx[NT];
         float f = c;
-        if (kind == kStepTail) {
+        if (kind == kStepTail && kBiasMfma) {
+            half_max<NT>(s, c, mx);
+        } else if (kind == kStepTail) {
             f = transform_tail(row, mt, s);
             half_max<NT>(s, f, mx);
         } else {
@@ -538,7 +580,10 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
             load_v_half(v0, 0);
         }
         pin_q();
-        scores_half(kf[0], sa);
+        {
+            const vec8 bf0 = kBiasMfma ? bias_frag(0, row0, 0) : ones_frag;
+            scores_half(kf[0], sa, kBiasMfma ? &bf0 : nullptr);
+        }
         load_k_half(kf[0], kptr(1, row1), 0);
         load_v_half(v0, 1);
         ca = check_half(0, row0, 0, sa, true, kStepGeneral);
@@ -567,7 +612,11 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
             vec8 pf[NT][2];
 
             // ---- first half: scores in sa (issued, masked and max-checked one half earlier)
-            if (!half0_only) scores_half(kf[1], sb);
+            if (!half0_only) {
+                // exact steps carry no bias MFMA (their chunks are exact blocks)
+                const vec8 bf1 = (kBiasMfma && !exact_k) ? bias_frag(cc, row0, 1) : ones_frag;
+                scores_half(kf[1], sb, (kBiasMfma && !exact_k) ? &bf1 : nullptr);
+            }
             probs_half<T, NT>(sa, ca, nm, l, lt, tail, pf);
             load_k_half(kf[1], kn, 1);
             pv_half(0, pf);
@@ -575,7 +624,10 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
             const float cb = half0_only ? c : check_half(cc, row0, 1, sb, true, kind);
 
             // ---- second half: scores in sb; also scores the next chunk's first half
-            if (!last) scores_half(kf[0], sa);
+            if (!last) {
+                const vec8 bf0 = (kBiasMfma && !exact_k) ? bias_frag(cc + 1, row1, 0) : ones_frag;
+                scores_half(kf[0], sa, (kBiasMfma && !exact_k) ? &bf0 : nullptr);
+            }
             if (!half0_only) probs_half<T, NT>(sb, cb, nm, l, lt, tail, pf);
             load_k_half(kf[0], kn2, 0);
             if (!half0_only) pv_half(1, pf);

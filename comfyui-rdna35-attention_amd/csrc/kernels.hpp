@@ -144,6 +144,7 @@ struct AttnArgs {
     TokenMap qmap;
     int q_tokens, kv_tokens, q_blocks, kv_blocks;
     float scale_log2;  // softmax scale * log2(e)
+    float inv_scale_log2;  // 1 / scale_log2 (centroid biases in score units)
     // sparse exact chunks
     const int32_t* idx;  // [BH][q_blocks][exact]
     int exact;
