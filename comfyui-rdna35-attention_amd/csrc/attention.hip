@@ -449,8 +449,9 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
                 for (int nt = 0; nt < NT; ++nt) o[md][nt] = mfma32(vf[md][2 * mt + ss], pf[nt][ss], o[md][nt]);
     };
     // Whether half chunks of chunk x (table row `row`) need transform_half: tail
-    // chunks and a short last key block (wave-uniform).
-    auto special = [&](int x, int row) { return is_tail(x) || (row + 1) * kBlock > a.kv_tokens; };
+    // chunks whose bias is not added by the matrix core, and a short last key
+    // block (wave-uniform).
+    auto special = [&](int x, int row) { return (!kBiasMfma && is_tail(x)) || (row + 1) * kBlock > a.kv_tokens; };
     // A operand of the bias MFMA of half mt of chunk x (table row `row`):
     // lane (0, col) holds the bias of centroid 64 row + 32 mt + col divided by
     // c, as bf16 hi and lo; every other slot is zero (all of them for an exact
