@@ -583,7 +583,7 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
         pin_q();
         {
             const vec8 bf0 = kBiasMfma ? bias_frag(0, row0, 0) : ones_frag;
-            scores_half(kf[0], sa, kBiasMfma ? &bf0 : nullptr);
+            scores_half(kf[0], sa, (kBiasMfma && is_tail(0)) ? &bf0 : nullptr);
         }
         load_k_half(kf[0], kptr(1, row1), 0);
         load_v_half(v0, 1);
@@ -614,9 +614,9 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
 
             // ---- first half: scores in sa (issued, masked and max-checked one half earlier)
             if (!half0_only) {
-                // exact steps carry no bias MFMA (their chunks are exact blocks)
+                // only centroid chunks carry the bias MFMA
                 const vec8 bf1 = (kBiasMfma && !exact_k) ? bias_frag(cc, row0, 1) : ones_frag;
-                scores_half(kf[1], sb, (kBiasMfma && !exact_k) ? &bf1 : nullptr);
+                scores_half(kf[1], sb, (kBiasMfma && (tail_k || (!exact_k && is_tail(cc)))) ? &bf1 : nullptr);
             }
             probs_half<T, NT>(sa, ca, nm, l, lt, tail, pf);
             load_k_half(kf[1], kn, 1);
@@ -627,7 +627,7 @@ __device__ __forceinline__ void attention_block(const AttnArgs& a, int bh, int q
             // ---- second half: scores in sb; also scores the next chunk's first half
             if (!last) {
                 const vec8 bf0 = (kBiasMfma && !exact_k) ? bias_frag(cc + 1, row1, 0) : ones_frag;
-                scores_half(kf[0], sa, (kBiasMfma && !exact_k) ? &bf0 : nullptr);
+                scores_half(kf[0], sa, (kBiasMfma && (tail_k || (!exact_k && is_tail(cc + 1)))) ? &bf0 : nullptr);
             }
             if (!half0_only) probs_half<T, NT>(sb, cb, nm, l, lt, tail, pf);
             load_k_half(kf[0], kn2, 0);
