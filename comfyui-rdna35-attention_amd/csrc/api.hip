@@ -824,6 +824,12 @@ int attn_hip_dense_forward(int32_t dtype, int32_t batch, int32_t heads, int32_t 
         return fail(PISA_ERR_UNSUPPORTED, "dense attention supports head_dim a multiple of 8 up to 256, got %d",
                     head_dim);
     if (!(scale > 0.0f) || scale == __builtin_inff()) return fail(PISA_ERR_INVALID_ARGUMENT, "scale must be positive and finite");
+    // the attention kernel addresses one head's packed key (value) table with
+    // 32-bit byte offsets in a buffer resource
+    const int64_t head_table_bytes = ((int64_t)kv_tokens + pisa::kBlock - 1) / pisa::kBlock * pisa::kBlock * padded * 2;
+    if (head_table_bytes > INT32_MAX)
+        return fail(PISA_ERR_UNSUPPORTED, "dense attention: Tk=%d at head_dim %d needs %lld bytes of packed keys per head, "
+                    "above 2 GiB", kv_tokens, head_dim, (long long)head_table_bytes);
     int rc;
     if ((rc = check_view("q", q, 2, true)) || (rc = check_view("k", k, 2, true)) || (rc = check_view("v", v, 2, true)) ||
         (rc = check_view("out", out, 2, false)))

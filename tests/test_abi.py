@@ -112,6 +112,9 @@ def test_other_entry_points_validate(lib):
     q, k, v, o = _views(lib)
     assert lib.LIB.attn_hip_dense_forward(0, 1, 1, 64, 64, 100, q, k, v, o, 0.1, None, 0, None) == 2
     assert lib.LIB.attn_hip_dense_forward(0, 1, 1, 64, 64, 264, q, k, v, o, 0.1, None, 0, None) == 2
+    # one head's packed key table above 2 GiB (32-bit offsets in the kernel) is refused before any launch
+    assert lib.LIB.attn_hip_dense_forward(0, 1, 1, 64, 1 << 23, 256, q, k, v, o, 0.1, None, 0, None) == 2
+    assert b"above 2 GiB" in lib.LIB.pisa_hip_last_error()
     assert lib.LIB.attn_hip_fixed_block_forward(0, 1, 1, 64, 48, 64, q, k, v, o, 0.1, 0, None) == 2
     assert lib.LIB.attn_hip_fixed_block_forward(0, 1, 1, 64, 64, 32, q, k, v, o, 0.1, 0, None) == 2
     assert lib.LIB.pisa_hip_route_topk(1, 2000, 128, None, None, None, 1, 0.1, -2, 3, None, None, None) == 2
