@@ -443,6 +443,47 @@ def test_fixed_block_replays_in_a_hip_graph(native, dtype):
         assert not torch.equal(other, eager)
 
 
+def _graph_calls(native):
+    from mi355x_pisa.synthetic import anima_qkv
+
+    spatial = anima_qkv(batch=1, heads=2, seed=11, device="cuda")
+    gen = torch.Generator().manual_seed(12)
+    video = [torch.randn((1, 3, 4096, D), generator=gen).to(torch.bfloat16).cuda() for _ in range(3)]
+    cross_q = torch.randn((1, 3, 1000, D), generator=gen).to(torch.bfloat16).cuda()
+    return {
+        "spatial": (lambda a, b, c: native.forward_spatial_bhtd(a, b, c, exact_blocks=23), spatial),
+        "generic": (lambda a, b, c: native.generic_forward(a, b, c, 10, D ** -0.5, True, token_grid=(4, 32, 32),
+                                                           stats="generic"), video),
+        "dense": (lambda a, b, c: native.dense_attention(a, b, c, D ** -0.5), (cross_q, video[1], video[2])),
+    }
+
+
+@pytest.mark.parametrize("call", ["spatial", "generic", "dense"])
+def test_forwards_replay_in_a_hip_graph(native, call):
+    """The PISA and dense entry points launch kernels on the caller's stream and nothing else
+    (no host synchronisation, no memset, workspace from the caller's allocator), so a caller can
+    capture a whole call in a HIP graph: every replay, with other eager work of the same entry
+    point and synchronisations between replays, equals the eager result bit for bit."""
+    fn, (q, k, v) = _graph_calls(native)[call]
+    eager = fn(q, k, v)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn(q, k, v)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        captured = fn(q, k, v)
+    for replay in range(4):
+        other = fn(q, v, k)  # eager work of the same shapes between replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(captured, eager), f"{call} replay {replay}"
+        assert not torch.equal(other, eager)
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_fixed_block_16bit_paths_on_large_and_unaligned_inputs(native, dtype):
     """Many blocks through the matrix-core kernel (B=2 H=16 T=4096 D=128, a ComfyUI-sized call),

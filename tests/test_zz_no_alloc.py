@@ -81,3 +81,34 @@ def test_noalloc_refuses_problems_beyond_the_scratch(lib):
                                                      lib.ROUTE_HYD, 1), torch.cuda.current_stream().cuda_stream)
     assert status == 3  # PISA_ERR_WORKSPACE, returned before any launch
     assert b"static scratch" in lib.LIB.pisa_hip_last_error()
+
+
+def test_noalloc_call_replays_in_a_hip_graph(lib):
+    """The callers this entry point serves are typically capturing: one call captured in a HIP graph
+    replays to the eager result bit for bit, with eager calls of another problem (which overwrite the
+    scratch) and synchronisations between the replays."""
+    q, k, v = _qkv(1, 4, 9216, seed=21)
+    eager = torch.empty((1, 4, 9216, D), dtype=torch.bfloat16, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    lib.check(lib.LIB.pisa_hip_forward_noalloc(*_args(lib, q, k, v, eager, (1, 96, 96), 23, lib.STATS_HYD,
+                                                      lib.ROUTE_HYD, 1), stream), "pisa_hip_forward_noalloc")
+    torch.cuda.synchronize()
+    assert torch.isfinite(eager).all()
+    replayed = torch.full_like(eager, float("nan"))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        status = lib.LIB.pisa_hip_forward_noalloc(
+            *_args(lib, q, k, v, replayed, (1, 96, 96), 23, lib.STATS_HYD, lib.ROUTE_HYD, 1),
+            torch.cuda.current_stream().cuda_stream)
+    assert status == 0, lib.LIB.pisa_hip_last_error()
+    q2, k2, v2 = _qkv(2, 2, 4096, seed=22)
+    other = torch.empty((2, 2, 4096, D), dtype=torch.bfloat16, device="cuda")
+    for replay in range(3):
+        lib.check(lib.LIB.pisa_hip_forward_noalloc(*_args(lib, q2, k2, v2, other, (1, 64, 64), 10,
+                                                          lib.STATS_GENERIC, lib.ROUTE_CENTROID, 1), stream),
+                  "pisa_hip_forward_noalloc")
+        torch.cuda.synchronize()
+        replayed.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(replayed, eager), f"replay {replay}"
