@@ -87,6 +87,23 @@ static int check_view(const char* name, const pisa_view& v, int esize, bool vec1
     return PISA_OK;
 }
 
+// Launch sizes: the block grids are 1-D with at most 256 threads per
+// workgroup (so below 2^24 workgroups the thread count stays under 2^32) and
+// the H_sum reductions run one grid row per head (at most 65535 rows).
+constexpr int64_t kMaxBatchHeads = 65535;
+constexpr int64_t kMaxGridBlocks = (int64_t(1) << 24) - 1;
+
+static bool sizes_fit(int32_t batch, int32_t heads, int32_t tokens) {
+    const int64_t bh = (int64_t)batch * heads;
+    return bh <= kMaxBatchHeads && bh * (((int64_t)tokens + pisa::kBlock - 1) / pisa::kBlock) <= kMaxGridBlocks;
+}
+
+static int check_sizes(const char* what, int32_t batch, int32_t heads, int32_t tokens) {
+    if (sizes_fit(batch, heads, tokens)) return PISA_OK;
+    return fail(PISA_ERR_UNSUPPORTED, "%s supports B*H <= %lld and B*H*ceil(T/64) <= %lld blocks, got B=%d H=%d T=%d",
+                what, (long long)kMaxBatchHeads, (long long)kMaxGridBlocks, batch, heads, tokens);
+}
+
 static int check_grid(const pisa_token_grid& g, int tokens) {
     if (g.frames <= 0) return PISA_OK;
     if (g.height <= 0 || g.width <= 0 || g.height % 8 || g.width % 8)
@@ -259,7 +276,7 @@ int pisa_hip_build_info(char* buffer, int64_t capacity) {
 
 int64_t pisa_hip_forward_workspace_bytes(int32_t batch, int32_t heads, int32_t tokens, int32_t head_dim,
                                          int32_t exact_blocks) {
-    if (batch <= 0 || heads <= 0 || tokens <= 0 || head_dim <= 0) return 0;
+    if (batch <= 0 || heads <= 0 || tokens <= 0 || head_dim <= 0 || !sizes_fit(batch, heads, tokens)) return 0;
     return carve_forward(nullptr, batch * heads, tokens, head_dim, exact_blocks, 2).total;
 }
 
@@ -276,6 +293,8 @@ static int validate_forward(int32_t dtype, int32_t batch, int32_t heads, int32_t
     if (!valid_dtype(dtype)) return fail(PISA_ERR_UNSUPPORTED, "PISA forward supports bf16 and fp16 only");
     if (batch <= 0 || heads <= 0 || tokens <= 0)
         return fail(PISA_ERR_INVALID_ARGUMENT, "PISA forward requires B>0, H>0, T>0");
+    int rc;
+    if ((rc = check_sizes("PISA forward", batch, heads, tokens))) return rc;
     if (head_dim != 128) {
         // other head dims take the Triton statistics (generic_pisa.py:128-138,
         // pisa_kernel.py:90-130: any head dim up to 256, H_sum included) and
@@ -302,7 +321,6 @@ static int validate_forward(int32_t dtype, int32_t batch, int32_t heads, int32_t
         return fail(PISA_ERR_INVALID_ARGUMENT, "stats_mode must be HYD or GENERIC");
     if (route_mode != PISA_ROUTE_HYD && route_mode != PISA_ROUTE_CENTROID)
         return fail(PISA_ERR_INVALID_ARGUMENT, "route_mode must be HYD or CENTROID");
-    int rc;
     if ((rc = check_grid(grid, tokens)) || (rc = check_view("q", q, 2, true)) || (rc = check_view("k", k, 2, true)) ||
         (rc = check_view("v", v, 2, true)) || (rc = check_view("out", out, 2, false)))
         return rc;
@@ -596,7 +614,7 @@ static int stats_padded_dim(int head_dim) {
 }
 
 int64_t pisa_hip_block_stats_workspace_bytes(int32_t batch, int32_t heads, int32_t tokens, int32_t head_dim) {
-    if (batch <= 0 || heads <= 0 || tokens <= 0 || head_dim <= 0) return 0;
+    if (batch <= 0 || heads <= 0 || tokens <= 0 || head_dim <= 0 || !sizes_fit(batch, heads, tokens)) return 0;
     const StatsPlan p = plan_stats(batch * heads, tokens);
     if (head_dim == 128) return (int64_t)batch * heads * p.chunks * head_dim * head_dim * 4;
     const int padded = stats_padded_dim(head_dim);
@@ -613,6 +631,8 @@ int pisa_hip_block_stats(int32_t dtype, int32_t out_dtype, int32_t batch, int32_
     if (out_dtype != dtype && out_dtype != PISA_DTYPE_F32)
         return fail(PISA_ERR_INVALID_ARGUMENT, "out_dtype must equal dtype or be float32");
     if (batch <= 0 || heads <= 0 || tokens <= 0) return fail(PISA_ERR_INVALID_ARGUMENT, "requires B>0, H>0, T>0");
+    int rc;
+    if ((rc = check_sizes("block statistics", batch, heads, tokens))) return rc;
     const bool value_sums = (stats_mode & PISA_STATS_FLAG_VALUE_SUMS) != 0;
     stats_mode &= ~PISA_STATS_FLAG_VALUE_SUMS;
     if (stats_mode != PISA_STATS_MEANS && stats_mode != PISA_STATS_HYD && stats_mode != PISA_STATS_GENERIC)
@@ -630,7 +650,6 @@ int pisa_hip_block_stats(int32_t dtype, int32_t out_dtype, int32_t batch, int32_
     // statistics form no norms), required at 128 where the kernel writes them
     if (cov && (!h_sum || (!h_norm && (stats_mode == PISA_STATS_HYD || head_dim == 128))))
         return fail(PISA_ERR_INVALID_ARGUMENT, "h_sum and h_norm are required");
-    int rc;
     // 16-byte row loads at widths that are multiples of 8; element loads otherwise
     const bool rows16 = head_dim % 8 == 0;
     if ((rc = check_grid(grid, tokens)) || (rc = check_view("q", q, 2, rows16)) ||
@@ -710,6 +729,8 @@ int pisa_hip_route_topk(int32_t batch_heads, int32_t blocks, int32_t head_dim, c
                         int32_t* indices, float* scores, void* stream) {
     if (batch_heads <= 0 || blocks <= 0) return fail(PISA_ERR_INVALID_ARGUMENT, "requires BH>0 and blocks>0");
     if (blocks > pisa::kMaxRouteBlocks) return fail(PISA_ERR_UNSUPPORTED, "at most %d blocks", pisa::kMaxRouteBlocks);
+    int rc;
+    if ((rc = check_sizes("routing", 1, batch_heads, blocks * pisa::kBlock))) return rc;
     if (head_dim <= 0 || head_dim > 256 || head_dim % 4)
         return fail(PISA_ERR_UNSUPPORTED, "head_dim must be a multiple of 4 in (0, 256]");
     if (exact_blocks < 0 || exact_blocks > blocks) return fail(PISA_ERR_INVALID_ARGUMENT, "exact_blocks out of range");
@@ -717,7 +738,6 @@ int pisa_hip_route_topk(int32_t batch_heads, int32_t blocks, int32_t head_dim, c
         return fail(PISA_ERR_INVALID_ARGUMENT, "sink_block must be None, -1, or 0");
     if (!qc || !kc || (!indices && exact_blocks > 0)) return fail(PISA_ERR_INVALID_ARGUMENT, "null pointer argument");
     if (!aligned16(kc)) return fail(PISA_ERR_INVALID_ARGUMENT, "kc must be 16-byte aligned");
-    int rc;
     if ((rc = check_device())) return rc;
     pisa::RouteArgs ro;
     ro.qc = qc;
@@ -748,6 +768,7 @@ int pisa_hip_pack_spatial_qkv(int32_t dtype, int32_t batch, int32_t heads, int32
     if (head_dim <= 0 || head_dim % 8 || head_dim > 2048)
         return fail(PISA_ERR_UNSUPPORTED, "head_dim must be a multiple of 8 (<= 2048)");
     int rc;
+    if ((rc = check_sizes("spatial layout", batch, heads, tokens))) return rc;
     if ((rc = check_grid(grid, tokens)) || (rc = check_view("q", q, 2, true)) || (rc = check_view("k", k, 2, true)) ||
         (rc = check_view("v", v, 2, true)))
         return rc;
@@ -776,6 +797,7 @@ int pisa_hip_unpack_spatial_output(int32_t dtype, int32_t batch, int32_t heads, 
     if (head_dim <= 0 || head_dim % 8 || head_dim > 2048)
         return fail(PISA_ERR_UNSUPPORTED, "head_dim must be a multiple of 8 (<= 2048)");
     int rc;
+    if ((rc = check_sizes("spatial layout", batch, heads, tokens))) return rc;
     if ((rc = check_grid(grid, tokens))) return rc;
     if (!packed || !raster || !aligned16(packed) || !aligned16(raster))
         return fail(PISA_ERR_INVALID_ARGUMENT, "packed and raster must be non-null and 16-byte aligned");
@@ -794,6 +816,7 @@ int pisa_hip_fuse_spatial_epilogue(int32_t dtype, int32_t batch, int32_t heads, 
     if (head_dim <= 0 || head_dim % 8 || head_dim > 2048)
         return fail(PISA_ERR_UNSUPPORTED, "head_dim must be a multiple of 8 (<= 2048)");
     int rc;
+    if ((rc = check_sizes("spatial layout", batch, heads, tokens))) return rc;
     if ((rc = check_grid(grid, tokens))) return rc;
     if (!exact_output || !exact_lse || !approximate_output || !approximate_lse || !correction || !out)
         return fail(PISA_ERR_INVALID_ARGUMENT, "null pointer argument");
@@ -807,7 +830,7 @@ int pisa_hip_fuse_spatial_epilogue(int32_t dtype, int32_t batch, int32_t heads, 
 }
 
 int64_t attn_hip_dense_workspace_bytes(int32_t batch, int32_t heads, int32_t kv_tokens, int32_t head_dim) {
-    if (batch <= 0 || heads <= 0 || kv_tokens <= 0 || head_dim <= 0) return 0;
+    if (batch <= 0 || heads <= 0 || kv_tokens <= 0 || head_dim <= 0 || !sizes_fit(batch, heads, kv_tokens)) return 0;
     const int64_t blocks = (kv_tokens + pisa::kBlock - 1) / pisa::kBlock;
     const int padded = pisa::padded_head_dim(head_dim) ? pisa::padded_head_dim(head_dim) : head_dim;
     return 2 * (int64_t)batch * heads * blocks * padded * pisa::kBlock * 2;  // packed K and V blocks
@@ -819,6 +842,10 @@ int attn_hip_dense_forward(int32_t dtype, int32_t batch, int32_t heads, int32_t 
     if (!valid_dtype(dtype)) return fail(PISA_ERR_UNSUPPORTED, "dense attention supports bf16 and fp16 only");
     if (batch <= 0 || heads <= 0 || q_tokens <= 0 || kv_tokens <= 0)
         return fail(PISA_ERR_INVALID_ARGUMENT, "requires B>0, H>0, Tq>0, Tk>0");
+    int rc;
+    if ((rc = check_sizes("dense attention", batch, heads, q_tokens)) ||
+        (rc = check_sizes("dense attention", batch, heads, kv_tokens)))
+        return rc;
     const int padded = pisa::padded_head_dim(head_dim);
     if (!padded)
         return fail(PISA_ERR_UNSUPPORTED, "dense attention supports head_dim a multiple of 8 up to 256, got %d",
@@ -830,7 +857,6 @@ int attn_hip_dense_forward(int32_t dtype, int32_t batch, int32_t heads, int32_t 
     if (head_table_bytes > INT32_MAX)
         return fail(PISA_ERR_UNSUPPORTED, "dense attention: Tk=%d at head_dim %d needs %lld bytes of packed keys per head, "
                     "above 2 GiB", kv_tokens, head_dim, (long long)head_table_bytes);
-    int rc;
     if ((rc = check_view("q", q, 2, true)) || (rc = check_view("k", k, 2, true)) || (rc = check_view("v", v, 2, true)) ||
         (rc = check_view("out", out, 2, false)))
         return rc;
@@ -874,6 +900,8 @@ int attn_hip_fixed_block_forward_masked(int32_t dtype, int32_t batch, int32_t he
         return fail(PISA_ERR_UNSUPPORTED, "fixed-block attention supports bf16, fp16 and fp32");
     if (batch <= 0 || heads <= 0 || tokens <= 0) return fail(PISA_ERR_INVALID_ARGUMENT, "requires B>0, H>0, T>0");
     if (block_size != 64) return fail(PISA_ERR_UNSUPPORTED, "fixed-block attention supports block_size=64 only");
+    int rc;
+    if ((rc = check_sizes("fixed-block attention", batch, heads, tokens))) return rc;
     if (head_dim != 32 && head_dim != 64 && head_dim != 128)
         return fail(PISA_ERR_UNSUPPORTED, "fixed-block attention supports head_dim 32/64/128, got %d", head_dim);
     if (!(scale == scale) || scale == __builtin_inff() || scale == -__builtin_inff())
@@ -888,7 +916,6 @@ int attn_hip_fixed_block_forward_masked(int32_t dtype, int32_t batch, int32_t he
             return fail(PISA_ERR_INVALID_ARGUMENT, "mask heads %d must divide B*H=%d", mask.heads, batch * heads);
     }
     const int es = elem_size(dtype);
-    int rc;
     if ((rc = check_view("q", q, es, false)) || (rc = check_view("k", k, es, false)) ||
         (rc = check_view("v", v, es, false)) || (rc = check_view("out", out, es, false)))
         return rc;

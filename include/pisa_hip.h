@@ -11,6 +11,10 @@
  * Every entry point returns PISA_OK (0) or a PISA_ERR_* code; a human readable
  * description of the last failure on the calling thread is available from
  * pisa_hip_last_error().  Validation failures never launch a kernel.
+ * Problem sizes: every entry point takes B*H <= 65535 and at most 2^24 - 1
+ * 64-token blocks over all heads (B*H*ceil(T/64), for dense attention both
+ * Tq and Tk); larger problems return PISA_ERR_UNSUPPORTED and the
+ * *_workspace_bytes functions return 0 for them.
  *
  * Reference interfaces replaced (paths relative to the reference repository):
  *   native/rdna35_pisa_ck/csrc/bindings.cpp:34-83          pybind module _C

@@ -115,6 +115,15 @@ def test_other_entry_points_validate(lib):
     # one head's packed key table above 2 GiB (32-bit offsets in the kernel) is refused before any launch
     assert lib.LIB.attn_hip_dense_forward(0, 1, 1, 64, 1 << 23, 256, q, k, v, o, 0.1, None, 0, None) == 2
     assert b"above 2 GiB" in lib.LIB.pisa_hip_last_error()
+    # B*H above 65535 or more than 2^24 - 1 blocks over all heads: refused before any launch, and the
+    # int32 product B*H is never formed for them
+    assert lib.LIB.attn_hip_dense_forward(0, 1 << 16, 1 << 16, 64, 64, 128, q, k, v, o, 0.1, None, 0, None) == 2
+    assert b"B*H <= 65535" in lib.LIB.pisa_hip_last_error()
+    assert lib.LIB.attn_hip_dense_forward(0, 4, 4096, 64, 1 << 16, 128, q, k, v, o, 0.1, None, 0, None) == 2
+    assert lib.LIB.attn_hip_dense_workspace_bytes(4, 4096, 1 << 16, 128) == 0
+    assert lib.LIB.attn_hip_fixed_block_forward(2, 1, 1, 1 << 30, 64, 64, q, k, v, o, 0.1, 0, None) == 2
+    assert lib.LIB.pisa_hip_forward_workspace_bytes(70000, 1, 64, 128, 0) == 0
+    assert lib.LIB.pisa_hip_block_stats_workspace_bytes(1, 70000, 64, 128) == 0
     assert lib.LIB.attn_hip_fixed_block_forward(0, 1, 1, 64, 48, 64, q, k, v, o, 0.1, 0, None) == 2
     assert lib.LIB.attn_hip_fixed_block_forward(0, 1, 1, 64, 64, 32, q, k, v, o, 0.1, 0, None) == 2
     assert lib.LIB.pisa_hip_route_topk(1, 2000, 128, None, None, None, 1, 0.1, -2, 3, None, None, None) == 2
