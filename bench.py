@@ -35,6 +35,12 @@ Also measured in the same process, in this order:
     beside the published peak the roofline uses;
   * the metric's region again right after one idle second
     (call_ms_after_1s_idle);
+  * unfused_pipeline: the reference's spatial pipeline on this library's
+    kernels (pack Q, K, V to 8x8-tile order, the contiguous [B*H, T, D]
+    forward, unpack to raster; __init__.py:406-433 of the reference's native
+    module), timed beside the fused call in one region, with the largest
+    difference between the two outputs: what reading and writing the raster
+    layout in place saves;
   * the CPU baseline: the fp32 torch port of the HYD forward
     (oracle.torch_cpu) over the whole call on the host's CPU threads.
 
@@ -616,6 +622,17 @@ def main() -> int:
     time.sleep(1.0)
     call_after_idle_ms = time_gpu(call, args.steps, args.warmup)
 
+    # the reference's unfused spatial pipeline on the same kernels, timed right beside the fused call
+    native = mi355x_pisa._C
+
+    def unfused():
+        pq, pk, pv = native.pack_spatial_qkv(q, k, v)
+        return native.unpack_spatial_output(mi355x_pisa.forward(pq, pk, pv, EXACT, scale), BATCH, HEADS)
+
+    unfused_diff = (unfused().float() - call().float()).abs().max().item()
+    unfused_ms = time_gpu(unfused, args.steps, args.warmup)
+    fused_again_ms = time_gpu(call, args.steps, args.warmup)
+
     chunk_ms = (attend_probe_ms - attend_ms) / (EXACT_PROBE - EXACT)
     chunk_flops = flops_per_exact_step()
     exact_tiles = {
@@ -665,6 +682,14 @@ def main() -> int:
         "call_effective_tflops": round(total_flops / (call_ms * 1e-3) / 1e12, 2),
         "stages_ms": {"prepare": round(prepare_ms, 4), "attend": round(attend_ms, 4)},
         "call_ms_after_1s_idle": round(call_after_idle_ms, 4),
+        "unfused_pipeline": {
+            "method": "pack_spatial_qkv + forward on [B*H,T,D] + unpack_spatial_output, HIP events, beside the "
+                      "fused call in one region",
+            "ms": round(unfused_ms, 4),
+            "fused_ms": round(fused_again_ms, 4),
+            "saved_ms": round(unfused_ms - fused_again_ms, 4),
+            "max_abs_diff": unfused_diff,
+        },
         "first_call_ms": round(first_call_ms, 3),
         "settle_calls": SETTLE_CALLS,
         "dense_ms": round(dense_ms, 4),
