@@ -32,6 +32,7 @@ MASK_BOOL = 1
 MASK_ADD_F32 = 2
 MASK_ADD_F16 = 3
 MASK_ADD_BF16 = 4
+NOALLOC_SCRATCH_BYTES = 192 << 20  # static scratch of pisa_hip_forward_noalloc
 
 _DTYPES = {torch.bfloat16: DTYPE_BF16, torch.float16: DTYPE_F16, torch.float32: DTYPE_F32}
 

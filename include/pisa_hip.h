@@ -207,21 +207,22 @@ PISA_HIP_EXPORT int pisa_hip_attend(int32_t dtype, int32_t batch, int32_t heads,
  * This entry point has no counterpart in the reference: it exists for callers
  * that cannot allocate device memory (code under HIP graph capture, tight
  * serving loops, hosts that forbid hipMalloc).  The workspace is a static
- * device array of PISA_NOALLOC_SCRATCH_BYTES (256 MiB) inside the library,
+ * device array of PISA_NOALLOC_SCRATCH_BYTES (192 MiB) inside the library,
  * one per GPU, held until the process ends.  The array belongs to the
  * library's code object, so every process that loads libpisa_hip.so holds
- * these 256 MiB on every GPU it uses the library on, whether or not it ever
+ * these 192 MiB on every GPU it uses the library on, whether or not it ever
  * calls this entry point.  A problem whose
  * pisa_hip_forward_workspace_bytes exceeds it is refused with
  * PISA_ERR_WORKSPACE before anything is launched (the Anima profile
- * B=2 H=16 T=9216 needs 197 MB).  No debug outputs.  Every call on one GPU
+ * B=2 H=16 T=9216 needs 187.3-189.4 MiB, at any exact-block count; the
+ * array is sized for it and no larger).  No debug outputs.  Every call on one GPU
  * uses that GPU's one array: calls that overlap on one GPU (two streams, two
  * host threads) race and must be serialised by the caller; calls in one
  * stream are ordered and safe.  Nothing in the array needs to start at zero
  * (every stage writes what it later reads), so no clearing is enqueued.
  * Arguments as pisa_hip_forward.
  */
-#define PISA_NOALLOC_SCRATCH_BYTES (256LL << 20)
+#define PISA_NOALLOC_SCRATCH_BYTES (192LL << 20)
 PISA_HIP_EXPORT int pisa_hip_forward_noalloc(int32_t dtype, int32_t batch, int32_t heads, int32_t tokens,
                              int32_t head_dim, pisa_view q, pisa_view k, pisa_view v, pisa_view out,
                              pisa_token_grid grid, int32_t exact_blocks, float scale, int32_t sink_block,

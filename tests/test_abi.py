@@ -223,3 +223,21 @@ def test_reference_stats_choice_through_the_alias_matches_generic_stats_mode(dty
     assert chosen == mi355x_pisa.generic_stats_mode(tokens, head_dim, dtype)
     expected = "hyd" if (dtype == torch.bfloat16 and head_dim == 128 and tokens <= 9216) else "generic"
     assert chosen == expected
+
+
+def test_noalloc_scratch_size_holds_the_anima_profile(lib):
+    """The header's PISA_NOALLOC_SCRATCH_BYTES, the binding's constant and the entry point's refusal agree,
+    and the static scratch holds the Anima profile (B=2 H=16 T=9216) at every exact-block count."""
+    define = re.search(r"#define\s+PISA_NOALLOC_SCRATCH_BYTES\s+\((\d+)LL\s*<<\s*(\d+)\)", HEADER.read_text())
+    assert define, "PISA_NOALLOC_SCRATCH_BYTES not found in the header"
+    scratch = int(define.group(1)) << int(define.group(2))
+    assert scratch == lib.NOALLOC_SCRATCH_BYTES
+    for exact in (0, 1, 23, 143):
+        assert lib.LIB.pisa_hip_forward_workspace_bytes(2, 16, 9216, 128, exact) <= scratch
+    assert lib.LIB.pisa_hip_forward_workspace_bytes(2, 17, 9216, 128, 23) > scratch
+    q, k, v, o = _views(lib)
+    # the size check comes before any device call: refused here, without a GPU
+    status = lib.LIB.pisa_hip_forward_noalloc(0, 2, 17, 9216, 128, q, k, v, o, lib.grid(1, 96, 96), 23, 0.088, -2, 1,
+                                              0, 1, None)
+    assert status == 3
+    assert b"static scratch" in lib.LIB.pisa_hip_last_error()
